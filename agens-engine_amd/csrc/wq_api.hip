@@ -1,0 +1,241 @@
+// GEMV entry points of the C ABI: argument rules, routing between the two numerics, token chunking and the
+// per-(device, stream) split-K scratch.
+//
+// Argument rules and return codes follow the reference (kernels/src/w4_gemv.cu:702-731, :852-876, :898-935,
+// :3265-3282): group in {64, 128} with k % group == 0, 1 <= nseg <= 4, 1 <= m <= 128; error 1 otherwise.
+#include <stdlib.h>
+#include <string.h>
+
+#include <map>
+#include <mutex>
+#include <utility>
+
+#include "agens_kernels.h"
+#include "wq_common.h"
+
+namespace agq {
+
+int exact_gemv(int bits, const void* x, int m, const Segs& g, int k, int group, int bf16w, hipStream_t s);
+int exact_ct_gemv(const void* x, const int32_t* packed, const void* scales, void* y, int n, int k, hipStream_t s);
+int i8_gemv(int bits, const void* x, int m, const Segs& g, int k, int group, float* part, unsigned* ctr,
+            hipStream_t s);
+
+namespace {
+
+constexpr int kMaxTokensPerLaunch = 16;
+
+int g_mode = -1;  // -1: environment (AGENS_W4_EXACT=1 selects the exact path), 0: exact, 1: integer MFMA
+int g_single_pass = 0;  // 1: every workgroup covers all stripes of its rows (no split-K scratch); same bits
+
+bool exact_mode() {
+  if (g_mode >= 0) return g_mode == 0;
+  static int env = -1;
+  if (env < 0) {
+    const char* v = getenv("AGENS_W4_EXACT");
+    env = (v && v[0] == '1') ? 1 : 0;
+  }
+  return env == 1;
+}
+
+bool group_ok(int k, int group) { return (group == 64 || group == 128) && k % group == 0 && k % 32 == 0; }
+
+Segs make_segs(int nseg, const void* const* wt, const void* const* st, void* const* y, const int* n, const int* ldy,
+               int pad) {
+  Segs g;
+  memset(&g, 0, sizeof(g));
+  g.nseg = nseg;
+  for (int i = 0, e = 0; i < nseg; ++i) {
+    g.wt[i] = wt[i];
+    g.st[i] = static_cast<const uint16_t*>(st[i]);
+    g.y[i] = static_cast<uint16_t*>(y[i]);
+    g.n[i] = n[i];
+    g.ldy[i] = ldy ? ldy[i] : n[i];
+    e += (n[i] + pad - 1) / pad * pad;
+    g.end[i] = e;
+  }
+  return g;
+}
+
+// split-K scratch of one (device, stream): stripe partials and one ticket per 64-row range (zeroed at allocation;
+// every launch leaves its tickets at zero).  Grown outside stream capture only; a launch that cannot get enough
+// scratch runs in direct mode (same bits, every workgroup covers all stripes of its rows).
+struct Scratch {
+  float* part = nullptr;
+  size_t part_cap = 0;
+  unsigned* ctr = nullptr;
+  size_t ctr_cap = 0;
+};
+std::mutex g_scratch_mu;
+std::map<std::pair<int, hipStream_t>, Scratch> g_scratch;
+
+void get_scratch(hipStream_t s, size_t part_floats, size_t tickets, float** part, unsigned** ctr) {
+  *part = nullptr, *ctr = nullptr;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  Scratch& sc = g_scratch[std::make_pair(dev, s)];
+  if (sc.part_cap < part_floats || sc.ctr_cap < tickets) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return;
+    if (sc.part_cap < part_floats) {
+      if (sc.part) {
+        hipStreamSynchronize(s);
+        hipFree(sc.part);
+      }
+      sc.part = nullptr, sc.part_cap = 0;
+      const size_t want = part_floats + part_floats / 2;
+      if (hipMalloc(reinterpret_cast<void**>(&sc.part), want * sizeof(float)) != hipSuccess) return;
+      sc.part_cap = want;
+    }
+    if (sc.ctr_cap < tickets) {
+      if (sc.ctr) {
+        hipStreamSynchronize(s);
+        hipFree(sc.ctr);
+      }
+      sc.ctr = nullptr, sc.ctr_cap = 0;
+      const size_t want = tickets + tickets / 2 + 64;
+      if (hipMalloc(reinterpret_cast<void**>(&sc.ctr), want * sizeof(unsigned)) != hipSuccess) return;
+      if (hipMemset(sc.ctr, 0, want * sizeof(unsigned)) != hipSuccess) {
+        hipFree(sc.ctr);
+        sc.ctr = nullptr;
+        return;
+      }
+      sc.ctr_cap = want;
+    }
+  }
+  *part = sc.part, *ctr = sc.ctr;
+}
+
+// one launch of the default path, m <= 16
+int run_i8(int bits, const void* x, int m, const Segs& g, int k, int group, hipStream_t s) {
+  const int nquad = kpad(k) / group / 4, P = nquad < 8 ? nquad : 8;
+  const int rows_pad = g.end[g.nseg - 1];
+  const int ranges = (rows_pad + 63) / 64;
+  float* part = nullptr;
+  unsigned* ctr = nullptr;
+  if (P > 1 && !g_single_pass) get_scratch(s, (size_t)P * m * rows_pad, (size_t)ranges, &part, &ctr);
+  return i8_gemv(bits, x, m, g, k, group, part, ctr, s);
+}
+
+int gemv(int bits, const void* x, int m, int nseg, const void* const* wt, const void* const* st, void* const* y,
+         const int* n, const int* ldy, int k, int group, int bf16w, bool force_default, hipStream_t s) {
+  if (!group_ok(k, group) || nseg < 1 || nseg > kMaxSegs || m < 1 || m > 128) return AK_INVALID;
+  if (bits < 2 || bits > 4 || !x || !wt || !st || !y || !n) return AK_INVALID;
+  for (int i = 0; i < nseg; ++i)
+    if (n[i] < 1 || !wt[i] || !st[i] || !y[i] || (ldy && ldy[i] < n[i])) return AK_INVALID;
+  const bool exact = bf16w || (!force_default && exact_mode());
+  for (int m0 = 0; m0 < m; m0 += kMaxTokensPerLaunch) {
+    const int mm = m - m0 < kMaxTokensPerLaunch ? m - m0 : kMaxTokensPerLaunch;
+    void* yy[kMaxSegs];
+    for (int i = 0; i < nseg; ++i)
+      yy[i] = static_cast<uint16_t*>(y[i]) + (size_t)m0 * (ldy ? ldy[i] : n[i]);
+    const void* xx = static_cast<const uint16_t*>(x) + (size_t)m0 * k;
+    const int e = exact ? exact_gemv(bits, xx, mm, make_segs(nseg, wt, st, yy, n, ldy, 1), k, group, bf16w, s)
+                        : run_i8(bits, xx, mm, make_segs(nseg, wt, st, yy, n, ldy, 16), k, group, s);
+    if (e) return e;
+  }
+  return 0;
+}
+
+}  // namespace
+}  // namespace agq
+
+using namespace agq;
+
+extern "C" {
+
+int ak_wq_gemv_kt_multi(int bits, const void* x, int m, int nseg, const void* const* wt, const void* const* st,
+                        void* const* y, const int* n, const int* ldy, int k, int group, int bf16w, void* stream) {
+  return gemv(bits, x, m, nseg, wt, st, y, n, ldy, k, group, bf16w, false, static_cast<hipStream_t>(stream));
+}
+
+int ak_w4_gemv_kt(const void* x, const void* wt, const void* st, void* y, int n, int k, int group, int bf16w,
+                  void* stream) {
+  return ak_wq_gemv_kt_multi(4, x, 1, 1, &wt, &st, &y, &n, nullptr, k, group, bf16w, stream);
+}
+
+int ak_w4_gemv_kt_multi(const void* x, int nseg, const void* const* wt, const void* const* st, void* const* y,
+                        const int* n, int k, int group, int bf16w, void* stream) {
+  return ak_wq_gemv_kt_multi(4, x, 1, nseg, wt, st, y, n, nullptr, k, group, bf16w, stream);
+}
+
+int ak_w4_gemv_kt_batched(const void* x, const void* wt, const void* st, void* y, int m, int n, int k, int group,
+                          int bf16w, void* stream) {
+  return ak_wq_gemv_kt_multi(4, x, m, 1, &wt, &st, &y, &n, nullptr, k, group, bf16w, stream);
+}
+
+int ak_w3_gemv_kt(const void* x, const void* wt, const void* st, void* y, int n, int k, int group, void* stream) {
+  return ak_wq_gemv_kt_multi(3, x, 1, 1, &wt, &st, &y, &n, nullptr, k, group, 0, stream);
+}
+
+int ak_w3_gemv_kt_multi(const void* x, int nseg, const void* const* wt, const void* const* st, void* const* y,
+                        const int* n, int k, int group, void* stream) {
+  return ak_wq_gemv_kt_multi(3, x, 1, nseg, wt, st, y, n, nullptr, k, group, 0, stream);
+}
+
+int ak_w3_gemv_kt_batched(const void* x, const void* wt, const void* st, void* y, int m, int n, int k, int group,
+                          void* stream) {
+  return ak_wq_gemv_kt_multi(3, x, m, 1, &wt, &st, &y, &n, nullptr, k, group, 0, stream);
+}
+
+// always the default (integer MFMA) numerics, whatever ak_w4_set_mma selected
+int ak_w4_mma_gemv(const void* x, const void* wt, const void* st, void* y, int m, int n, int k, int group,
+                   void* stream) {
+  return gemv(4, x, m, 1, &wt, &st, &y, &n, nullptr, k, group, 0, true, static_cast<hipStream_t>(stream));
+}
+
+// g128 KT conveniences of the reference: the exact numerics (their bits are the reference's tuning variants' bits)
+int ak_w4g128_gemv_kt_variant(int variant, const void* x, const void* wt, const void* st, void* y, int n, int k,
+                              void* stream) {
+  if (k % 128 != 0) return AK_INVALID;
+  switch (variant) {
+    case 11: case 12: case 21: case 22: case 41: break;
+    default: return AK_INVALID;
+  }
+  const Segs g = make_segs(1, &wt, &st, &y, &n, nullptr, 1);
+  return exact_gemv(4, x, 1, g, k, 128, 0, static_cast<hipStream_t>(stream));
+}
+
+int ak_w4g128_gemv_kt_bf16(const void* x, const void* wt, const void* st, void* y, int n, int k, void* stream) {
+  return ak_w4g128_gemv_kt_variant(21, x, wt, st, y, n, k, stream);
+}
+
+int ak_w4g128_gemv_kt_tune(int r, int u, int warps, int bps, const void* x, const void* wt, const void* st, void* y,
+                           int n, int k, void* stream) {
+  if ((r != 1 && r != 2 && r != 4) || (u != 1 && u != 2 && u != 4) || (warps != 4 && warps != 8 && warps != 16) ||
+      bps < 0)
+    return AK_INVALID;
+  return ak_w4g128_gemv_kt_variant(11, x, wt, st, y, n, k, stream);
+}
+
+int ak_w4g128_gemv_bf16_variant(int variant, const void* x, const int32_t* packed, const void* scales, void* y, int n,
+                                int k, void* stream) {
+  if (k % 128 != 0 || n < 1) return AK_INVALID;
+  switch (variant) {
+    case 11: case 12: case 14: case 21: case 22: case 41: case 42: break;
+    default: return AK_INVALID;
+  }
+  return exact_ct_gemv(x, packed, scales, y, n, k, static_cast<hipStream_t>(stream));
+}
+
+int ak_w4g128_gemv_bf16(const void* x, const int32_t* packed, const void* scales, void* y, int n, int k,
+                        void* stream) {
+  return ak_w4g128_gemv_bf16_variant(22, x, packed, scales, y, n, k, stream);
+}
+
+int ak_w4_set_mma(int mode) {
+  g_mode = mode < 0 ? -1 : (mode ? 1 : 0);
+  return 0;
+}
+// reference: selects a bit-identical kernel variant.  Here: rb > 0 forces the single-pass variant of the default
+// path (no split-K scratch, one workgroup per 64 rows); -1 / 0 restore the automatic choice.  Same bits either way.
+int ak_w4_set_lean(int rb) {
+  g_single_pass = rb > 0 ? 1 : 0;
+  return 0;
+}
+int ak_w4_set_tma(int stages) {
+  (void)stages;
+  return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,123 @@
+/* libagens_kernels (MI355X / gfx950 build): the C ABI of the mixed-bit group-quantized linear-layer path.
+ *
+ * Drop-in for the quantized-GEMV part of the reference's kernels/include/agens_kernels.h: same names, argument order,
+ * argument meaning and return codes, so crates/agens-cuda/src/lib.rs:9-35 (Rust FFI) and the model's linear()
+ * (kernels/m1/m1_model.cu:1857-1937) bind to it unchanged.  Each declaration cites the reference declaration it
+ * replaces.  Entry points of the reference header that are not part of this path are not exported.
+ *
+ * Conventions (reference header :1-2):
+ *   - every int-returning function returns 0 on success or an error code with the reference's numeric meaning:
+ *     1 = invalid value (bad shape / group, or a value that needs more bits than requested), 2 = out of memory,
+ *     other values are hipError_t codes;
+ *   - `stream` is a hipStream_t (NULL = the default stream); launches are asynchronous and stream-ordered;
+ *   - bf16 tensors are passed as void* (raw 16-bit patterns), the int4 container as int32_t words;
+ *   - the caller owns every buffer it passes; the library owns only per-(device, stream) split-K scratch.
+ */
+#pragma once
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------------------------------------- runtime
+ * reference: kernels/include/agens_kernels.h:17-30 (implemented in kernels/src/runtime.cu:25-44). */
+int ak_device_count(int* n);                                  /* agens_kernels.h:17 */
+int ak_set_device(int dev);                                   /* agens_kernels.h:18 */
+int ak_device_name(int dev, char* buf, int len);              /* agens_kernels.h:19 */
+int ak_malloc(void** ptr, size_t bytes);                      /* agens_kernels.h:20 */
+int ak_free(void* ptr);                                       /* agens_kernels.h:21 */
+int ak_memcpy_h2d(void* dst, const void* src, size_t bytes);  /* agens_kernels.h:22 */
+int ak_memcpy_d2h(void* dst, const void* src, size_t bytes);  /* agens_kernels.h:23 */
+int ak_synchronize(void);                                     /* agens_kernels.h:24 */
+int ak_mem_info(size_t* free_bytes, size_t* total_bytes);     /* agens_kernels.h:25 */
+const char* ak_error_string(int code);                        /* agens_kernels.h:28 */
+int ak_host_alloc(void** ptr, size_t bytes);                  /* agens_kernels.h:29: pinned host memory */
+int ak_host_free(void* ptr);                                  /* agens_kernels.h:30 */
+
+/* ---------------------------------------------------------------------------------------------- sizes
+ * KT ("k-tiled") layout: k padded to kp = ceil(k / 1024) * 1024; tile t of row o is one record at
+ * (t * n + o) * (128 * bits) bytes; scales bf16 at (t * n + o) * (1024 / group).  reference: w4_gemv.cu:13-31. */
+size_t ak_w4_kt_weight_bytes(int n, int k);               /* agens_kernels.h:192, w4_gemv.cu:560 */
+size_t ak_w4_kt_scale_bytes(int n, int k, int group);     /* agens_kernels.h:193, w4_gemv.cu:561 */
+size_t ak_w3_kt_weight_bytes(int n, int k);               /* agens_kernels.h:240, w4_gemv.cu:822 */
+size_t ak_wq_kt_weight_bytes(int bits, int n, int k);     /* agens_kernels.h:255, w4_gemv.cu:821 */
+size_t ak_w4g128_kt_weight_bytes(int n, int k);           /* agens_kernels.h:181, w4_gemv.cu:562 */
+size_t ak_w4g128_kt_scale_bytes(int n, int k);            /* agens_kernels.h:182, w4_gemv.cu:563 */
+
+/* ---------------------------------------------------------------------------------------------- load-time repack
+ * int4 container (packed int32 [n][k/8], nibble = q + 8, low nibble first; scales bf16 [n][k/group]) -> KT.
+ * group in {64, 128}, k % group == 0, k % 32 == 0, else 1.  W3 / W2: 1 if a value needs more bits (the layout is
+ * written anyway; the caller keeps the linear wider).  The W3 / W2 entry points synchronize the stream. */
+int ak_w4_repack_kt(const int32_t* packed, const void* scales, void* wt, void* st, int n, int k, int group,
+                    void* stream);                        /* agens_kernels.h:194, w4_gemv.cu:565-583 */
+int ak_w3_repack_kt(const int32_t* packed, const void* scales, void* wt, void* st, int n, int k, int group,
+                    void* stream);                        /* agens_kernels.h:241, w4_gemv.cu:845-848 */
+int ak_wq_repack_kt(int bits, const int32_t* packed, const void* scales, void* wt, void* st, int n, int k, int group,
+                    void* stream);                        /* agens_kernels.h:256-257, w4_gemv.cu:826-844 */
+int ak_w4g128_repack_kt(const int32_t* packed, const void* scales, void* wt, void* st, int n, int k,
+                        void* stream);                    /* agens_kernels.h:183, w4_gemv.cu:585-588 */
+
+/* ---------------------------------------------------------------------------------------------- GEMV / small-M GEMM
+ * x bf16 [m][k] (rows contiguous, stride k, 16-byte aligned); y bf16, token j of segment i at y[i] + j * ldy[i]
+ * (ldy == NULL: n[i]).  1 <= m <= 128, 1 <= nseg <= 4, the segments share x, k, group and bits.
+ * Numerics (both deterministic; every output row is bit-identical for any m, any segmentation and any bit width
+ * holding the same values):
+ *   default  -- integer MFMA: exact per-group integer dot products of q with x, rounded once to fp32, scaled and
+ *               accumulated in fp32 in a fixed order;
+ *   exact    -- the reference's fp32 FMA path, bit for bit (ak_w4_set_mma(0) or AGENS_W4_EXACT=1);
+ *   bf16w=1  -- weights rounded to bf16(q * scale) first (Marlin numerics), always on the fp32 path. */
+int ak_wq_gemv_kt_multi(int bits, const void* x, int m, int nseg, const void* const* wt, const void* const* st,
+                        void* const* y, const int* n, const int* ldy, int k, int group, int bf16w,
+                        void* stream);            /* agens_kernels.h:258-259, w4_gemv.cu:852-876 */
+int ak_w4_gemv_kt(const void* x, const void* wt, const void* st, void* y, int n, int k, int group, int bf16w,
+                  void* stream);                  /* agens_kernels.h:195-196, w4_gemv.cu:702-710 */
+int ak_w4_gemv_kt_multi(const void* x, int nseg, const void* const* wt, const void* const* st, void* const* y,
+                        const int* n, int k, int group, int bf16w, void* stream); /* agens_kernels.h:197-198, w4_gemv.cu:712-720 */
+int ak_w4_gemv_kt_batched(const void* x, const void* wt, const void* st, void* y, int m, int n, int k, int group,
+                          int bf16w, void* stream); /* agens_kernels.h:199-200, w4_gemv.cu:722-731 */
+int ak_w3_gemv_kt(const void* x, const void* wt, const void* st, void* y, int n, int k, int group,
+                  void* stream);                  /* agens_kernels.h:242 */
+int ak_w3_gemv_kt_multi(const void* x, int nseg, const void* const* wt, const void* const* st, void* const* y,
+                        const int* n, int k, int group, void* stream); /* agens_kernels.h:243-244 */
+int ak_w3_gemv_kt_batched(const void* x, const void* wt, const void* st, void* y, int m, int n, int k, int group,
+                          void* stream);          /* agens_kernels.h:245-246 */
+/* reference: the tensor-core entry point (agens_kernels.h:204, w4_gemv.cu:3265-3270); here: the default numerics */
+int ak_w4_mma_gemv(const void* x, const void* wt, const void* st, void* y, int m, int n, int k, int group,
+                   void* stream);
+/* g128 conveniences (agens_kernels.h:184, :48-49): KT and the legacy int4-container (CT) GEMV, exact numerics */
+int ak_w4g128_gemv_kt_bf16(const void* x, const void* wt, const void* st, void* y, int n, int k, void* stream);
+int ak_w4g128_gemv_bf16(const void* x, const int32_t* packed, const void* scales, void* y, int n, int k,
+                        void* stream);
+/* tuning entries (agens_kernels.h:271-277, w4_gemv.cu:590-651, :916-935): every variant returns the same bits */
+int ak_w4g128_gemv_bf16_variant(int variant, const void* x, const int32_t* packed, const void* scales, void* y,
+                                int n, int k, void* stream);
+int ak_w4g128_gemv_kt_variant(int variant, const void* x, const void* wt, const void* st, void* y, int n, int k,
+                              void* stream);
+int ak_w4g128_gemv_kt_tune(int r, int u, int warps, int bps, const void* x, const void* wt, const void* st, void* y,
+                           int n, int k, void* stream);
+
+/* ---------------------------------------------------------------------------------------------- dequant (prefill)
+ * rows [r0, r0 + nr) -> w bf16 [nr][k], value bf16_rn(q * scale), bitwise.  reference: w4_gemv.cu:460-493. */
+int ak_wq_dequant_kt_rows(int bits, const void* wt, const void* st, void* w, int n, int k, int group, int r0, int nr,
+                          void* stream);          /* agens_kernels.h:260-261, w4_gemv.cu:877-895 */
+int ak_w4_dequant_kt(const void* wt, const void* st, void* w, int n, int k, int group,
+                     void* stream);               /* agens_kernels.h:265, w4_gemv.cu:733-741 */
+int ak_w4_dequant_kt_rows(const void* wt, const void* st, void* w, int n, int k, int group, int r0, int nr,
+                          void* stream);          /* agens_kernels.h:267-268, w4_gemv.cu:743-752 */
+int ak_w3_dequant_kt_rows(const void* wt, const void* st, void* w, int n, int k, int group, int r0, int nr,
+                          void* stream);          /* agens_kernels.h:247-248 */
+
+/* ---------------------------------------------------------------------------------------------- switches
+ * reference: agens_kernels.h:205 / :208 / :211, w4_gemv.cu:3271-3282.  mma: -1 auto (environment AGENS_W4_EXACT), 0 exact
+ * fp32 path, 1 default integer-MFMA path.  lean: rb > 0 forces the single-pass variant of the default path (no
+ * split-K scratch; same bits), -1 / 0 automatic.  tma selects an sm90-only variant in the reference; accepted and
+ * ignored here. */
+int ak_w4_set_mma(int mode);
+int ak_w4_set_lean(int rb);
+int ak_w4_set_tma(int stages);
+
+#ifdef __cplusplus
+}
+#endif

@@ -1,0 +1,64 @@
+"""CPU checks of the C-ABI library: it loads, exports every function include/agens_kernels.h declares, and its host
+logic (sizes, argument validation, switches) answers without a GPU."""
+import ctypes
+
+import pytest
+
+from _lib import kernels, header_symbols, oracle, KERNELS_SO
+
+
+@pytest.fixture(scope="module")
+def K():
+    import os
+    if not os.path.exists(KERNELS_SO):
+        import subprocess, sys
+        subprocess.run([sys.executable, os.path.join(os.path.dirname(KERNELS_SO), "build.py")], check=True)
+    return kernels()
+
+
+def test_exports_every_declared_symbol(K):
+    syms = header_symbols()
+    assert len(syms) >= 40
+    missing = [s for s in syms if not hasattr(K, s)]
+    assert not missing, missing
+
+
+def test_sizes_match_layout(K):
+    O = oracle()
+    for n, k in ((5120, 5120), (55296, 5120), (5120, 27648), (301, 1152), (77, 640)):
+        for bits in (2, 3, 4):
+            assert K.ak_wq_kt_weight_bytes(bits, n, k) == O.ora_kt_weight_bytes(bits, n, k)
+        assert K.ak_w4_kt_weight_bytes(n, k) == O.ora_kt_weight_bytes(4, n, k)
+        assert K.ak_w3_kt_weight_bytes(n, k) == O.ora_kt_weight_bytes(3, n, k)
+        for g in (64, 128):
+            assert K.ak_w4_kt_scale_bytes(n, k, g) == O.ora_kt_scale_bytes(n, k, g)
+    # BASELINE config 1 / 2 sizes: W3 55296 x 5120 and W2 5120 x 27648
+    assert K.ak_wq_kt_weight_bytes(3, 55296, 5120) == 106168320
+    assert K.ak_w4_kt_scale_bytes(55296, 5120, 128) == 4423680
+    assert K.ak_wq_kt_weight_bytes(2, 5120, 27648) == 35389440
+    assert K.ak_w4_kt_scale_bytes(5120, 27648, 128) == 2211840
+
+
+def test_invalid_arguments_return_1_without_a_gpu(K):
+    # w4_gemv.cu:556, :714, :724, :855 (and :565 / :826 for repack): bad group / k / nseg / m / bits -> 1
+    nul = ctypes.c_void_p(0)
+    arr = (ctypes.c_void_p * 1)(1)
+    n = (ctypes.c_int * 1)(16)
+    assert K.ak_wq_gemv_kt_multi(4, arr[0], 1, 1, arr, arr, arr, n, None, 1024, 96, 0, None) == 1   # group
+    assert K.ak_wq_gemv_kt_multi(4, arr[0], 1, 1, arr, arr, arr, n, None, 1000, 128, 0, None) == 1  # k % group
+    assert K.ak_wq_gemv_kt_multi(4, arr[0], 1, 5, arr, arr, arr, n, None, 1024, 128, 0, None) == 1  # nseg
+    assert K.ak_wq_gemv_kt_multi(4, arr[0], 0, 1, arr, arr, arr, n, None, 1024, 128, 0, None) == 1  # m
+    assert K.ak_wq_gemv_kt_multi(4, arr[0], 129, 1, arr, arr, arr, n, None, 1024, 128, 0, None) == 1
+    assert K.ak_wq_gemv_kt_multi(5, arr[0], 1, 1, arr, arr, arr, n, None, 1024, 128, 0, None) == 1  # bits
+    assert K.ak_wq_repack_kt(5, nul, nul, nul, nul, 16, 1024, 128, None) == 1
+    assert K.ak_w4_repack_kt(nul, nul, nul, nul, 16, 1000, 128, None) == 1
+    assert K.ak_wq_dequant_kt_rows(4, nul, nul, nul, 16, 1024, 128, 10, 10, None) == 1  # r0 + nr > n
+    assert K.ak_w4g128_gemv_kt_variant(33, nul, nul, nul, nul, 16, 1024, None) == 1
+    assert K.ak_w4g128_gemv_kt_tune(3, 1, 8, 0, nul, nul, nul, nul, 16, 1024, None) == 1
+
+
+def test_switches(K):
+    assert K.ak_w4_set_mma(0) == 0 and K.ak_w4_set_mma(1) == 0 and K.ak_w4_set_mma(-1) == 0
+    assert K.ak_w4_set_lean(2) == 0 and K.ak_w4_set_lean(-1) == 0
+    assert K.ak_w4_set_tma(4) == 0 and K.ak_w4_set_tma(-1) == 0
+    assert K.ak_error_string(1)
