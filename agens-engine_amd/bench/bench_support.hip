@@ -1,0 +1,236 @@
+// Benchmark support for bench.py (not part of the product ABI): device-side synthetic data in the reference's int4
+// container, a stream-read ceiling probe, and a native launcher that replays a list of GEMV launches (eager or as
+// one captured hipGraph) and times it with HIP events on its own stream.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string.h>
+
+#include <vector>
+
+#include "agens_kernels.h"
+
+namespace {
+
+__device__ __forceinline__ uint32_t mix(uint64_t seed, uint64_t index) {
+  uint64_t z = seed * 0x9E3779B97F4A7C15ull + index * 0xD1B54A32D192ED03ull + 0x632BE59BD9B4E019ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return (uint32_t)((z ^ (z >> 31)) >> 16);
+}
+
+__device__ __forceinline__ float normal(uint64_t seed, uint64_t i) {
+  const float u1 = ((float)mix(seed, 2 * i) + 1.0f) * 2.3283064e-10f;
+  const float u2 = (float)mix(seed, 2 * i + 1) * 2.3283064e-10f;
+  return sqrtf(-2.0f * logf(u1)) * cosf(6.2831853f * u2);
+}
+
+__device__ __forceinline__ uint16_t to_bf16(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+
+__global__ void gen_container_kernel(uint64_t seed, size_t words, int lo, int span, uint32_t* p) {
+  for (size_t w = blockIdx.x * (size_t)blockDim.x + threadIdx.x; w < words; w += (size_t)gridDim.x * blockDim.x) {
+    const uint32_t h0 = mix(seed, 2 * w), h1 = mix(seed, 2 * w + 1);
+    uint32_t v = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t r = ((j < 4 ? h0 : h1) >> (8 * (j & 3))) & 0xFFu;  // 8 random bits per code
+      const int q = lo + (int)((r * (uint32_t)span) >> 8);
+      v |= (uint32_t)(q + 8) << (4 * j);
+    }
+    p[w] = v;
+  }
+}
+
+__global__ void gen_scales_kernel(uint64_t seed, size_t count, float sa, float sb, uint16_t* s) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < count; i += (size_t)gridDim.x * blockDim.x)
+    s[i] = to_bf16(fabsf(normal(seed, i)) * sa + sb);
+}
+
+__global__ void gen_x_kernel(uint64_t seed, size_t count, float xs, uint16_t* x) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < count; i += (size_t)gridDim.x * blockDim.x)
+    x[i] = to_bf16(normal(seed, i) * xs);
+}
+
+__global__ void read_kernel(const uint4* __restrict__ p, size_t n16, uint32_t* out) {
+  uint32_t acc = 0;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n16; i += (size_t)gridDim.x * blockDim.x) {
+    typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+    const u4 v = __builtin_nontemporal_load(reinterpret_cast<const u4*>(p + i));
+    acc ^= v.x ^ v.y ^ v.z ^ v.w;
+  }
+  if (acc == 0x9E3779B9u) out[0] = acc;
+}
+
+__global__ void copy_kernel(const uint4* __restrict__ a, uint4* __restrict__ b, size_t n16) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n16; i += (size_t)gridDim.x * blockDim.x)
+    b[i] = a[i];
+}
+
+unsigned grid_for(size_t items) {
+  const size_t b = (items + 255) / 256;
+  return (unsigned)(b < 8192 ? (b ? b : 1) : 8192);
+}
+
+}  // namespace
+
+extern "C" {
+
+struct AgbLaunch {
+  int bits, m, nseg, k, group, bf16w;
+  const void* x;
+  const void* wt[4];
+  const void* st[4];
+  void* y[4];
+  int n[4];
+  int ldy[4];
+  int use_ldy;
+  int pad;
+};
+
+int agb_gen_container(uint64_t seed, int n, int k, int lo, int span, void* packed, void* stream) {
+  const size_t words = (size_t)n * k / 8;
+  hipLaunchKernelGGL(gen_container_kernel, dim3(grid_for(words)), dim3(256), 0, (hipStream_t)stream, seed, words, lo,
+                     span, (uint32_t*)packed);
+  return (int)hipGetLastError();
+}
+
+int agb_gen_scales(uint64_t seed, size_t count, float sa, float sb, void* s, void* stream) {
+  hipLaunchKernelGGL(gen_scales_kernel, dim3(grid_for(count)), dim3(256), 0, (hipStream_t)stream, seed, count, sa, sb,
+                     (uint16_t*)s);
+  return (int)hipGetLastError();
+}
+
+int agb_gen_x(uint64_t seed, size_t count, float xs, void* x, void* stream) {
+  hipLaunchKernelGGL(gen_x_kernel, dim3(grid_for(count)), dim3(256), 0, (hipStream_t)stream, seed, count, xs,
+                     (uint16_t*)x);
+  return (int)hipGetLastError();
+}
+
+static int launch_one(const AgbLaunch& L, hipStream_t s) {
+  return ak_wq_gemv_kt_multi(L.bits, L.x, L.m, L.nseg, L.wt, L.st, L.y, L.n, L.use_ldy ? L.ldy : nullptr, L.k,
+                             L.group, L.bf16w, s);
+}
+
+// Replays plan[0..nlaunch) `warmup` times untimed, then `steps` times between two events; *ms = elapsed / steps.
+// use_graph: the plan is captured once into a hipGraph (after the warmup) and each step is one graph launch.
+int agb_run(const AgbLaunch* plan, int nlaunch, int warmup, int steps, int use_graph, float* ms) {
+  hipStream_t s;
+  int e = (int)hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+  if (e) return e;
+  hipEvent_t a, b;
+  hipEventCreate(&a);
+  hipEventCreate(&b);
+  hipGraphExec_t ge = nullptr;
+  hipGraph_t g = nullptr;
+  for (int w = 0; w < (warmup > 0 ? warmup : 1) && !e; ++w)
+    for (int i = 0; i < nlaunch && !e; ++i) e = launch_one(plan[i], s);
+  if (!e) e = (int)hipStreamSynchronize(s);
+  if (!e && use_graph) {
+    e = (int)hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+    for (int i = 0; i < nlaunch && !e; ++i) e = launch_one(plan[i], s);
+    const int e2 = (int)hipStreamEndCapture(s, &g);
+    if (!e) e = e2;
+    if (!e) e = (int)hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+    if (!e) e = (int)hipGraphLaunch(ge, s);
+    if (!e) e = (int)hipStreamSynchronize(s);
+  }
+  if (!e) {
+    hipEventRecord(a, s);
+    for (int st = 0; st < steps && !e; ++st) {
+      if (use_graph) e = (int)hipGraphLaunch(ge, s);
+      else
+        for (int i = 0; i < nlaunch && !e; ++i) e = launch_one(plan[i], s);
+    }
+    hipEventRecord(b, s);
+    if (!e) e = (int)hipEventSynchronize(b);
+    float t = 0.f;
+    if (!e) e = (int)hipEventElapsedTime(&t, a, b);
+    *ms = steps > 0 ? t / steps : 0.f;
+  }
+  if (ge) hipGraphExecDestroy(ge);
+  if (g) hipGraphDestroy(g);
+  hipEventDestroy(a);
+  hipEventDestroy(b);
+  hipStreamSynchronize(s);
+  hipStreamDestroy(s);
+  return e;
+}
+
+// Duration of every launch of the plan (average over `reps` passes), each bracketed by its own pair of events on the
+// launching stream; ms_each[i] in milliseconds.
+int agb_time_each(const AgbLaunch* plan, int nlaunch, int reps, float* ms_each) {
+  hipStream_t s;
+  int e = (int)hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+  if (e) return e;
+  std::vector<hipEvent_t> ev(2 * (size_t)nlaunch);
+  for (auto& x : ev) hipEventCreate(&x);
+  for (int i = 0; i < nlaunch; ++i) ms_each[i] = 0.f;
+  for (int r = 0; r < reps && !e; ++r) {
+    for (int i = 0; i < nlaunch && !e; ++i) {
+      hipEventRecord(ev[2 * i], s);
+      e = launch_one(plan[i], s);
+      hipEventRecord(ev[2 * i + 1], s);
+    }
+    if (!e) e = (int)hipStreamSynchronize(s);
+    for (int i = 0; i < nlaunch && !e; ++i) {
+      float t = 0.f;
+      e = (int)hipEventElapsedTime(&t, ev[2 * i], ev[2 * i + 1]);
+      ms_each[i] += t / reps;
+    }
+  }
+  for (auto& x : ev) hipEventDestroy(x);
+  hipStreamDestroy(s);
+  return e;
+}
+
+// Stream-read ceiling: 16-byte nontemporal loads over `bytes` (>= 1 GB beats the 256 MB last-level cache).
+int agb_read_bw(size_t bytes, int reps, float* gbps) {
+  void* buf = nullptr;
+  void* sink = nullptr;
+  int e = (int)hipMalloc(&buf, bytes);
+  if (!e) e = (int)hipMalloc(&sink, 16);
+  if (!e) e = (int)hipMemset(buf, 1, bytes);
+  hipEvent_t a, b;
+  hipEventCreate(&a);
+  hipEventCreate(&b);
+  float best = 0.f;
+  for (int blocks : {2048, 4096}) {
+    if (e) break;
+    hipLaunchKernelGGL(read_kernel, dim3(blocks), dim3(512), 0, 0, (const uint4*)buf, bytes / 16, (uint32_t*)sink);
+    hipEventRecord(a, 0);
+    for (int r = 0; r < reps; ++r)
+      hipLaunchKernelGGL(read_kernel, dim3(blocks), dim3(512), 0, 0, (const uint4*)buf, bytes / 16, (uint32_t*)sink);
+    hipEventRecord(b, 0);
+    e = (int)hipEventSynchronize(b);
+    float t = 0.f;
+    hipEventElapsedTime(&t, a, b);
+    const float g = (float)((double)bytes * reps / (t * 1e6));
+    if (g > best) best = g;
+  }
+  *gbps = best;
+  hipEventDestroy(a);
+  hipEventDestroy(b);
+  if (buf) hipFree(buf);
+  if (sink) hipFree(sink);
+  return e;
+}
+
+// A plain copy of `bytes` (read + write), the calibration kernel for the HBM traffic counters.
+int agb_copy(size_t bytes, int reps) {
+  void *a = nullptr, *b = nullptr;
+  int e = (int)hipMalloc(&a, bytes);
+  if (!e) e = (int)hipMalloc(&b, bytes);
+  if (!e) e = (int)hipMemset(a, 3, bytes);
+  for (int r = 0; r < reps && !e; ++r) {
+    hipLaunchKernelGGL(copy_kernel, dim3(4096), dim3(256), 0, 0, (const uint4*)a, (uint4*)b, bytes / 16);
+    e = (int)hipGetLastError();
+  }
+  if (!e) e = (int)hipDeviceSynchronize();
+  if (a) hipFree(a);
+  if (b) hipFree(b);
+  return e;
+}
+
+}  // extern "C"

@@ -15,7 +15,8 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libagens_kernels.so")
-SOURCES = ["ak_runtime.hip", "wq_layout.hip", "wq_exact.hip", "wq_i8.hip", "wq_api.hip"]
+BENCH_LIB = os.path.join(HERE, "libagens_bench.so")
+SOURCES = ["ak_runtime.hip", "wq_layout.hip", "wq_exact.hip", "wq_i8.hip", "wq_i8m1.hip", "wq_api.hip"]
 
 
 def hipcc():
@@ -35,8 +36,9 @@ def flags():
 
 
 def _compile(src):
-    obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
-    cmd = [hipcc()] + flags() + ["-c", os.path.join(CSRC, src), "-o", obj]
+    obj = os.path.join(BUILD, os.path.basename(os.path.splitext(src)[0]) + ".o")
+    path = src if os.path.isabs(src) else os.path.join(CSRC, src)
+    cmd = [hipcc()] + flags() + ["-c", path, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     errs = "\n".join(l for l in (r.stdout + r.stderr).splitlines()
                      if "packed-fp32-ops" not in l and "not a recognized feature" not in l)
@@ -56,8 +58,17 @@ def build(jobs=None, verbose=True):
     if r.returncode != 0:
         raise RuntimeError("link failed:\n" + r.stdout + r.stderr)
     os.replace(tmp, LIB)
+    # benchmark support (bench.py only; not part of the product ABI), linked against the library
+    bobj = _compile(os.path.join(HERE, "bench", "bench_support.hip"))
+    tmp = BENCH_LIB + ".tmp"
+    cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", "-Wl,--no-undefined", "-o", tmp, bobj,
+           "-L" + HERE, "-lagens_kernels", "-Wl,-rpath,$ORIGIN"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("link failed (bench support):\n" + r.stdout + r.stderr)
+    os.replace(tmp, BENCH_LIB)
     if verbose:
-        print(f"built {LIB}")
+        print(f"built {LIB} and {BENCH_LIB}")
     return LIB
 
 

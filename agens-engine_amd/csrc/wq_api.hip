@@ -1,14 +1,11 @@
-// GEMV entry points of the C ABI: argument rules, routing between the two numerics, token chunking and the
-// per-(device, stream) split-K scratch.
+// GEMV entry points of the C ABI: argument rules, routing between the two numerics and token chunking.  The kernels
+// use no scratch memory: every launch is self-contained (stripe partials meet in LDS), so the entry points allocate
+// nothing and are safe under stream capture.
 //
 // Argument rules and return codes follow the reference (kernels/src/w4_gemv.cu:702-731, :852-876, :898-935,
 // :3265-3282): group in {64, 128} with k % group == 0, 1 <= nseg <= 4, 1 <= m <= 128; error 1 otherwise.
 #include <stdlib.h>
 #include <string.h>
-
-#include <map>
-#include <mutex>
-#include <utility>
 
 #include "agens_kernels.h"
 #include "wq_common.h"
@@ -17,15 +14,14 @@ namespace agq {
 
 int exact_gemv(int bits, const void* x, int m, const Segs& g, int k, int group, int bf16w, hipStream_t s);
 int exact_ct_gemv(const void* x, const int32_t* packed, const void* scales, void* y, int n, int k, hipStream_t s);
-int i8_gemv(int bits, const void* x, int m, const Segs& g, int k, int group, float* part, unsigned* ctr,
-            hipStream_t s);
+int i8_gemv(int bits, const void* x, int m, const Segs& g, int k, int group, hipStream_t s);
+int i8_gemv_m1(int bits, const void* x, const Segs& g, int k, int group, hipStream_t s);
 
 namespace {
 
 constexpr int kMaxTokensPerLaunch = 16;
 
 int g_mode = -1;  // -1: environment (AGENS_W4_EXACT=1 selects the exact path), 0: exact, 1: integer MFMA
-int g_single_pass = 0;  // 1: every workgroup covers all stripes of its rows (no split-K scratch); same bits
 
 bool exact_mode() {
   if (g_mode >= 0) return g_mode == 0;
@@ -56,65 +52,13 @@ Segs make_segs(int nseg, const void* const* wt, const void* const* st, void* con
   return g;
 }
 
-// split-K scratch of one (device, stream): stripe partials and one ticket per 64-row range (zeroed at allocation;
-// every launch leaves its tickets at zero).  Grown outside stream capture only; a launch that cannot get enough
-// scratch runs in direct mode (same bits, every workgroup covers all stripes of its rows).
-struct Scratch {
-  float* part = nullptr;
-  size_t part_cap = 0;
-  unsigned* ctr = nullptr;
-  size_t ctr_cap = 0;
-};
-std::mutex g_scratch_mu;
-std::map<std::pair<int, hipStream_t>, Scratch> g_scratch;
-
-void get_scratch(hipStream_t s, size_t part_floats, size_t tickets, float** part, unsigned** ctr) {
-  *part = nullptr, *ctr = nullptr;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return;
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
-  Scratch& sc = g_scratch[std::make_pair(dev, s)];
-  if (sc.part_cap < part_floats || sc.ctr_cap < tickets) {
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(s, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return;
-    if (sc.part_cap < part_floats) {
-      if (sc.part) {
-        hipStreamSynchronize(s);
-        hipFree(sc.part);
-      }
-      sc.part = nullptr, sc.part_cap = 0;
-      const size_t want = part_floats + part_floats / 2;
-      if (hipMalloc(reinterpret_cast<void**>(&sc.part), want * sizeof(float)) != hipSuccess) return;
-      sc.part_cap = want;
-    }
-    if (sc.ctr_cap < tickets) {
-      if (sc.ctr) {
-        hipStreamSynchronize(s);
-        hipFree(sc.ctr);
-      }
-      sc.ctr = nullptr, sc.ctr_cap = 0;
-      const size_t want = tickets + tickets / 2 + 64;
-      if (hipMalloc(reinterpret_cast<void**>(&sc.ctr), want * sizeof(unsigned)) != hipSuccess) return;
-      if (hipMemset(sc.ctr, 0, want * sizeof(unsigned)) != hipSuccess) {
-        hipFree(sc.ctr);
-        sc.ctr = nullptr;
-        return;
-      }
-      sc.ctr_cap = want;
-    }
-  }
-  *part = sc.part, *ctr = sc.ctr;
-}
-
-// one launch of the default path, m <= 16
+// one launch of the default path, m <= 16 (one token: the decode kernel, when its activations fit the LDS)
 int run_i8(int bits, const void* x, int m, const Segs& g, int k, int group, hipStream_t s) {
-  const int nquad = kpad(k) / group / 4, P = nquad < 8 ? nquad : 8;
-  const int rows_pad = g.end[g.nseg - 1];
-  const int ranges = (rows_pad + 63) / 64;
-  float* part = nullptr;
-  unsigned* ctr = nullptr;
-  if (P > 1 && !g_single_pass) get_scratch(s, (size_t)P * m * rows_pad, (size_t)ranges, &part, &ctr);
-  return i8_gemv(bits, x, m, g, k, group, part, ctr, s);
+  if (m == 1) {
+    const int e = i8_gemv_m1(bits, x, g, k, group, s);
+    if (e != AK_INVALID) return e;
+  }
+  return i8_gemv(bits, x, m, g, k, group, s);
 }
 
 int gemv(int bits, const void* x, int m, int nseg, const void* const* wt, const void* const* st, void* const* y,
@@ -227,10 +171,9 @@ int ak_w4_set_mma(int mode) {
   g_mode = mode < 0 ? -1 : (mode ? 1 : 0);
   return 0;
 }
-// reference: selects a bit-identical kernel variant.  Here: rb > 0 forces the single-pass variant of the default
-// path (no split-K scratch, one workgroup per 64 rows); -1 / 0 restore the automatic choice.  Same bits either way.
+// reference: selects a bit-identical sm90 kernel variant; one default kernel family here, so accepted and ignored
 int ak_w4_set_lean(int rb) {
-  g_single_pass = rb > 0 ? 1 : 0;
+  (void)rb;
   return 0;
 }
 int ak_w4_set_tma(int stages) {

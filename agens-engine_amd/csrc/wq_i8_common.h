@@ -1,0 +1,157 @@
+// Device helpers shared by the integer-MFMA GEMV kernels (wq_i8.hip: any m; wq_i8m1.hip: m = 1).
+// The numerics they implement are described at the top of wq_i8.hip.
+#pragma once
+#include "wq_common.h"
+
+namespace agq {
+
+struct I8Args {
+  Segs segs;
+  const uint16_t* x;
+  int m, k;
+  int nquad, P;   // quads of the padded k, stripes
+  int nb;         // quads per LDS batch (any-m kernel)
+  int iters_max;  // row-block iterations per workgroup (m = 1 kernel)
+};
+
+namespace {
+
+__device__ __forceinline__ uint32_t byte_of(uint32_t v, int j) { return (v >> (8 * j)) & 0xFFu; }
+
+template <int BITS>
+constexpr int code_offset() { return BITS == 4 ? 8 : BITS == 3 ? 4 : 2; }
+
+// -OFF in every byte: the constant B operand that turns sum(d * n) into sum(d * q)
+template <int BITS>
+constexpr int neg_off_bytes() { return BITS == 4 ? (int)0xF8F8F8F8u : BITS == 3 ? (int)0xFCFCFCFCu : (int)0xFEFEFEFEu; }
+
+template <int BITS>
+struct Raw;
+template <>
+struct Raw<4> { uint4 w; };
+template <>
+struct Raw<3> { uint2 lo; uint32_t hi; };
+template <>
+struct Raw<2> { uint2 lo; };
+
+template <int BITS>
+__device__ __forceinline__ Raw<BITS> load_raw(const void* __restrict__ wt, size_t rec, int c) {
+  Raw<BITS> r;
+  if constexpr (BITS == 4) {
+    r.w = ld_stream(reinterpret_cast<const uint4*>(wt) + rec * 32 + c);
+  } else {
+    const uint32_t* p = reinterpret_cast<const uint32_t*>(wt) + rec * (32 * BITS);
+    r.lo = ld_stream2(reinterpret_cast<const uint2*>(p) + c);
+    if constexpr (BITS == 3) r.hi = ld_stream1(p + 64 + c);
+  }
+  return r;
+}
+
+// The two B operands (16 int8 codes each) of one lane chunk.  Input o (0..31) of the chunk lands at
+//   W4: half o % 2, VGPR o / 8, byte (o % 8) / 2;  W2: half o / 16, VGPR o % 4, byte (o % 16) / 4;
+//   W3: half (o % 8) / 4, VGPR o % 4, byte o / 8.
+template <int BITS>
+__device__ __forceinline__ void make_b(const Raw<BITS>& r, i32x4& b0, i32x4& b1) {
+  if constexpr (BITS == 4) {
+    const uint32_t w[4] = {r.w.x, r.w.y, r.w.z, r.w.w};
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      b0[v] = (int)(w[v] & 0x0F0F0F0Fu);
+      b1[v] = (int)((w[v] >> 4) & 0x0F0F0F0Fu);
+    }
+  } else if constexpr (BITS == 2) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      b0[s] = (int)((r.lo.x >> (2 * s)) & 0x03030303u);
+      b1[s] = (int)((r.lo.y >> (2 * s)) & 0x03030303u);
+    }
+  } else {
+    const uint32_t L0 = r.lo.x, L1 = r.lo.y, H = r.hi;
+    // bytes m of P0 / P1 hold the 2-bit fields of inputs 8m .. 8m+3 / 8m+4 .. 8m+7
+    const uint32_t P0 = (L0 & 0xFFu) | ((L0 >> 8) & 0xFF00u) | ((L1 & 0xFFu) << 16) | ((L1 << 8) & 0xFF000000u);
+    const uint32_t P1 = ((L0 >> 8) & 0xFFu) | ((L0 >> 16) & 0xFF00u) | ((L1 << 8) & 0xFF0000u) | (L1 & 0xFF000000u);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      b0[t] = (int)(((P0 >> (2 * t)) & 0x03030303u) | (((H >> t) & 0x01010101u) << 2));
+      b1[t] = (int)(((P1 >> (2 * t)) & 0x03030303u) | (((H >> (t + 4)) & 0x01010101u) << 2));
+    }
+  }
+}
+
+// The group's limb sums -> fp32: T = D2 * 256 + D1 (exact int32), gsum = fmaf((float)T, 256, (float)D0), i.e.
+// fp32_rn(GS) whenever |T| < 2^24 (always but for adversarial data).  The caller multiplies by scale * 2^(E - 148).
+__device__ __forceinline__ float group_sum_f32(const i32x4& d) {
+  const int t = d[2] * 256 + d[1];
+  return fmaf((float)t, 256.0f, (float)d[0]);
+}
+
+// 2^(E - 148) as fp32 bits (the activation scale of a group whose largest exponent field is E)
+__device__ __forceinline__ int act_scale_bits(int e) { return __float_as_int(ldexpf(1.0f, e - 148)); }
+
+// One group's activation limbs from 8 consecutive bf16 inputs per lane, LPU lanes per group: the group's largest
+// exponent field e (all LPU lanes) and, per input, x_int = trunc(x * 2^(148 - e)) with its three limb-byte sources.
+template <int LPU>
+__device__ __forceinline__ int group_limbs(const uint4 v, uint32_t (&t0)[8], uint32_t (&t1)[8], uint32_t (&t2)[8]) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  int e = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) e = max(e, max((int)((w[i] >> 7) & 0xFFu), (int)((w[i] >> 23) & 0xFFu)));
+#pragma unroll
+  for (int o = 1; o < LPU; o <<= 1) e = max(e, __shfl_xor(e, o));
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t b16 = (w[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
+    const int xi = (int)ldexpf(bf2f(b16), 148 - e);  // exact; truncation toward zero
+    t0[i] = (uint32_t)xi;                            // limb 0 = byte 0
+    t1[i] = (uint32_t)xi + 0x80u;                    // limb 1 = byte 1
+    t2[i] = (uint32_t)xi + 0x8080u;                  // limb 2 = byte 2
+  }
+  return e;
+}
+
+// Writes the limb bytes of inputs o0 .. o0+7 of a lane chunk: dst points at (chunk, half 0, limb 0) of the LDS operand
+// layout, half_stride = bytes between half 0 and half 1 (limb rows are 16 bytes apart).
+template <int BITS>
+__device__ __forceinline__ void store_limbs(uint8_t* dst, size_t half_stride, int o0, const uint32_t (&t0)[8],
+                                            const uint32_t (&t1)[8], const uint32_t (&t2)[8]) {
+  if constexpr (BITS == 4) {
+    // word v = o0 / 8: even inputs -> half 0 bytes 0..3, odd -> half 1
+    const int v4 = o0 >> 3;
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+      for (int limb = 0; limb < 3; ++limb) {
+        const uint32_t* t = limb == 0 ? t0 : limb == 1 ? t1 : t2;
+        const uint32_t d = byte_of(t[hf], limb) | (byte_of(t[hf + 2], limb) << 8) | (byte_of(t[hf + 4], limb) << 16) |
+                           (byte_of(t[hf + 6], limb) << 24);
+        *reinterpret_cast<uint32_t*>(dst + hf * half_stride + limb * 16 + 4 * v4) = d;
+      }
+  } else if constexpr (BITS == 2) {
+    // half o0 / 16, VGPR i % 4, byte 2 * ((o0 / 8) % 2) + i / 4
+    const int hf = o0 >> 4, bb = 2 * ((o0 >> 3) & 1);
+#pragma unroll
+    for (int limb = 0; limb < 3; ++limb) {
+      const uint32_t* t = limb == 0 ? t0 : limb == 1 ? t1 : t2;
+#pragma unroll
+      for (int vv = 0; vv < 4; ++vv) {
+        const uint16_t d = (uint16_t)(byte_of(t[vv], limb) | (byte_of(t[vv + 4], limb) << 8));
+        *reinterpret_cast<uint16_t*>(dst + hf * half_stride + limb * 16 + 4 * vv + bb) = d;
+      }
+    }
+  } else {
+    // W3: half i / 4, VGPR i % 4, byte o0 / 8
+    const int bb = o0 >> 3;
+#pragma unroll
+    for (int limb = 0; limb < 3; ++limb) {
+      const uint32_t* t = limb == 0 ? t0 : limb == 1 ? t1 : t2;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        dst[(i >> 2) * half_stride + limb * 16 + 4 * (i & 3) + bb] = (uint8_t)byte_of(t[i], limb);
+    }
+  }
+}
+
+
+
+}  // namespace
+}  // namespace agq

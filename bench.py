@@ -1,0 +1,351 @@
+#!/usr/bin/env python3
+"""Benchmark of the mixed-bit quantized GEMV path on one MI355X.
+
+Headline (BASELINE.json metric): effective HBM GB/s (and % of the 8 TB/s peak) and microseconds per 64-layer
+32B-shaped decode GEMV sweep at M = 1: per layer QKV (5120 -> 7168 as q/k/v segments of one launch), O (5120 -> 5120),
+gate_up (5120 -> 55296) and down (27648 -> 5120), each layer's bit width drawn from a fixed seed (W2 p=.3, W3 p=.5,
+W4 p=.2), group 128, plus the W4 LM head (5120 -> 152064).  One "step" = one sweep (257 GEMV launches), replayed as
+one hipGraph (the engine runs decode inside captured graphs).  Weights are generated on the device in the
+reference's int4 container and repacked by ak_wq_repack_kt; inputs are resident in HBM before the timed region.
+
+Effective bytes per launch = packed weights + bf16 scales + bf16 x + bf16 y (the algorithmic bytes).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--m 1] [--config sweep|0|1|2|3] [--no-cpu] [--eager]
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "agens-engine_amd")
+HBM_PEAK_GBS = 8000.0
+SEED = 20261201
+
+
+class AgbLaunch(ctypes.Structure):
+    _fields_ = [("bits", ctypes.c_int), ("m", ctypes.c_int), ("nseg", ctypes.c_int), ("k", ctypes.c_int),
+                ("group", ctypes.c_int), ("bf16w", ctypes.c_int), ("x", ctypes.c_void_p),
+                ("wt", ctypes.c_void_p * 4), ("st", ctypes.c_void_p * 4), ("y", ctypes.c_void_p * 4),
+                ("n", ctypes.c_int * 4), ("ldy", ctypes.c_int * 4), ("use_ldy", ctypes.c_int), ("pad", ctypes.c_int)]
+
+
+def load_libs():
+    kso = os.path.join(PKG, "libagens_kernels.so")
+    bso = os.path.join(PKG, "libagens_bench.so")
+    if not (os.path.exists(kso) and os.path.exists(bso)):
+        raise SystemExit(f"{kso} / {bso} missing: run `python agens-engine_amd/build.py` first")
+    K = ctypes.CDLL(kso)
+    B = ctypes.CDLL(bso)
+    vp, i, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
+    for name, res, args in [
+        ("ak_malloc", i, [ctypes.POINTER(vp), sz]), ("ak_free", i, [vp]), ("ak_memcpy_d2h", i, [vp, vp, sz]),
+        ("ak_synchronize", i, []), ("ak_wq_kt_weight_bytes", sz, [i, i, i]),
+        ("ak_w4_kt_scale_bytes", sz, [i, i, i]), ("ak_wq_repack_kt", i, [i, vp, vp, vp, vp, i, i, i, vp]),
+        ("ak_device_name", i, [i, ctypes.c_char_p, i]), ("ak_error_string", ctypes.c_char_p, [i]),
+    ]:
+        f = getattr(K, name)
+        f.restype, f.argtypes = res, args
+    for name, res, args in [
+        ("agb_gen_container", i, [ctypes.c_uint64, i, i, i, i, vp, vp]),
+        ("agb_gen_scales", i, [ctypes.c_uint64, sz, ctypes.c_float, ctypes.c_float, vp, vp]),
+        ("agb_gen_x", i, [ctypes.c_uint64, sz, ctypes.c_float, vp, vp]),
+        ("agb_run", i, [ctypes.POINTER(AgbLaunch), i, i, i, i, ctypes.POINTER(ctypes.c_float)]),
+        ("agb_time_each", i, [ctypes.POINTER(AgbLaunch), i, i, ctypes.POINTER(ctypes.c_float)]),
+        ("agb_read_bw", i, [sz, i, ctypes.POINTER(ctypes.c_float)]),
+    ]:
+        f = getattr(B, name)
+        f.restype, f.argtypes = res, args
+    return K, B
+
+
+class Ctx:
+    def __init__(self, K, B):
+        self.K, self.B, self.bufs = K, B, []
+
+    def check(self, rc, what):
+        if rc:
+            raise RuntimeError(f"{what}: error {rc} ({self.K.ak_error_string(rc).decode()})")
+
+    def alloc(self, nbytes, keep=True):
+        p = ctypes.c_void_p()
+        self.check(self.K.ak_malloc(ctypes.byref(p), max(int(nbytes), 16)), "ak_malloc")
+        if keep:
+            self.bufs.append(p)
+        return p
+
+    def free(self, p):
+        self.K.ak_free(p)
+
+    def free_all(self):
+        for p in self.bufs:
+            self.K.ak_free(p)
+        self.bufs = []
+
+
+def code_range(bits):
+    return -(1 << (bits - 1)), 1 << bits
+
+
+class QLinear:
+    """A quantized linear generated on the device: container (temporary) -> KT via ak_wq_repack_kt."""
+
+    def __init__(self, ctx, seed, n, k, bits, group=128, ct=None, cs=None, keep_container=False):
+        K, B = ctx.K, ctx.B
+        self.n, self.k, self.bits, self.group, self.seed = n, k, bits, group, seed
+        self.wbytes = K.ak_wq_kt_weight_bytes(bits, n, k)
+        self.sbytes = K.ak_w4_kt_scale_bytes(n, k, group)
+        self.wt = ctx.alloc(self.wbytes)
+        self.st = ctx.alloc(self.sbytes)
+        own = ct is None
+        if own:
+            ct = ctx.alloc(n * k // 2, keep=False)
+            cs = ctx.alloc(n * k // group * 2, keep=False)
+        lo, span = code_range(bits)
+        ctx.check(B.agb_gen_container(seed, n, k, lo, span, ct, None), "gen container")
+        ctx.check(B.agb_gen_scales(seed + 1, n * k // group, 0.02, 1e-4, cs, None), "gen scales")
+        ctx.check(K.ak_wq_repack_kt(bits, ct, cs, self.wt, self.st, n, k, group, None), "repack")
+        self.container = None
+        if keep_container:  # host copy of the container for the CPU baseline
+            p = np.zeros(n * k // 8, dtype=np.uint32)
+            s = np.zeros(n * k // group, dtype=np.uint16)
+            ctx.check(K.ak_synchronize(), "sync")
+            ctx.check(K.ak_memcpy_d2h(p.ctypes.data, ct, p.nbytes), "d2h")
+            ctx.check(K.ak_memcpy_d2h(s.ctypes.data, cs, s.nbytes), "d2h")
+            self.container = (p, s)
+        if own:
+            ctx.check(K.ak_synchronize(), "sync")
+            ctx.free(ct)
+            ctx.free(cs)
+
+
+def launch(bits, m, k, x, segs, ys, group=128):
+    L = AgbLaunch()
+    L.bits, L.m, L.nseg, L.k, L.group, L.bf16w = bits, m, len(segs), k, group, 0
+    L.x = x.value
+    for i, (lin, y) in enumerate(zip(segs, ys)):
+        L.wt[i], L.st[i], L.y[i], L.n[i] = lin.wt.value, lin.st.value, y.value, lin.n
+    L.use_ldy = 0
+    return L
+
+
+def algo_bytes(L):
+    b = 0
+    for i in range(L.nseg):
+        n = L.n[i]
+        b += n * ((L.k + 1023) // 1024 * 1024) * L.bits // 8 + n * ((L.k + 1023) // 1024 * 1024) // L.group * 2
+        b += L.m * n * 2
+    return b + L.m * L.k * 2
+
+
+def layer_bits(layer):
+    """Per-layer bit width from the seed: W2 p=0.3, W3 p=0.5, W4 p=0.2."""
+    u = (np.random.default_rng([SEED, layer]).random())
+    return 2 if u < 0.3 else (3 if u < 0.8 else 4)
+
+
+def build_sweep(ctx, m, cpu_layers):
+    """64 layers + LM head; returns (plan, meta, containers for the CPU baseline)."""
+    H, KV, INTER, VOCAB = 5120, 1024, 27648, 152064
+    B = ctx.B
+    # staging for the containers (largest: LM head 152064 x 5120)
+    ct = ctx.alloc(VOCAB * H // 2, keep=False)
+    cs = ctx.alloc(VOCAB * H // 128 * 2, keep=False)
+    xh = ctx.alloc(m * H * 2)
+    xd = ctx.alloc(m * INTER * 2)
+    ctx.check(B.agb_gen_x(SEED + 1, m * H, 1.0, xh, None), "gen x")
+    ctx.check(B.agb_gen_x(SEED + 2, m * INTER, 1.0, xd, None), "gen x")
+    yq, yk, yv = ctx.alloc(m * H * 2), ctx.alloc(m * KV * 2), ctx.alloc(m * KV * 2)
+    yo, yg, ydn = ctx.alloc(m * H * 2), ctx.alloc(m * 2 * INTER * 2), ctx.alloc(m * H * 2)
+    ylm = ctx.alloc(m * VOCAB * 2)
+    plan, meta, cpu = [], [], []
+    for l in range(64):
+        b = layer_bits(l)
+        s = SEED * 1000 + 10 * l
+        keep = l < cpu_layers
+        q = QLinear(ctx, s + 0, H, H, b, ct=ct, cs=cs, keep_container=keep)
+        kk = QLinear(ctx, s + 2, KV, H, b, ct=ct, cs=cs, keep_container=keep)
+        v = QLinear(ctx, s + 4, KV, H, b, ct=ct, cs=cs, keep_container=keep)
+        o = QLinear(ctx, s + 6, H, H, b, ct=ct, cs=cs, keep_container=keep)
+        gu = QLinear(ctx, s + 8, 2 * INTER, H, b, ct=ct, cs=cs, keep_container=keep)
+        dn = QLinear(ctx, s + 10, H, INTER, b, ct=ct, cs=cs, keep_container=keep)
+        plan += [launch(b, m, H, xh, [q, kk, v], [yq, yk, yv]), launch(b, m, H, xh, [o], [yo]),
+                 launch(b, m, H, xh, [gu], [yg]), launch(b, m, INTER, xd, [dn], [ydn])]
+        meta += [("qkv", b), ("o", b), ("gate_up", b), ("down", b)]
+        if keep:
+            cpu += [(xh, H, [q, kk, v]), (xh, H, [o]), (xh, H, [gu]), (xd, INTER, [dn])]
+    lm = QLinear(ctx, SEED * 1000 + 999, VOCAB, H, 4, ct=ct, cs=cs)
+    plan.append(launch(4, m, H, xh, [lm], [ylm]))
+    meta.append(("lm_head", 4))
+    ctx.check(ctx.K.ak_synchronize(), "sync")
+    ctx.free(ct)
+    ctx.free(cs)
+    return plan, meta, cpu
+
+
+def cpu_baseline(ctx, m, cpu, budget_s=20.0):
+    """The reference's CPU path (reference.rs:53-71, restated in C by the oracle: per-group fp32 sums) on the first
+    layers of the same sweep, single thread, timed on this host; GB/s of the same algorithmic bytes."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from _lib import oracle, ptr  # the checker / baseline leg (test infrastructure)
+    O = oracle()
+    K = ctx.K
+    xs = {}
+    t_total, bytes_total, nlin = 0.0, 0, 0
+    for x, k, lins in cpu:
+        key = (x.value, k)
+        if key not in xs:
+            xh = np.zeros(m * k, dtype=np.uint16)
+            ctx.check(K.ak_memcpy_d2h(xh.ctypes.data, x, xh.nbytes), "d2h")
+            xs[key] = xh
+        xh = xs[key]
+        for lin in lins:
+            p, s = lin.container
+            y = np.zeros(m * lin.n, dtype=np.float32)
+            t0 = time.perf_counter()
+            O.ora_gemv_ref_f32(ptr(xh), m, ptr(p), ptr(s), ptr(y), lin.n, lin.n, k, 128, 1)
+            t_total += time.perf_counter() - t0
+            bytes_total += lin.wbytes + lin.sbytes + m * lin.n * 2
+            nlin += 1
+        bytes_total += m * k * 2
+        if t_total > budget_s:
+            break
+    return {"value": round(bytes_total / t_total / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{nlin} linears of the sweep's first layers (M={m}), reference CPU path restated in C "
+                      f"(oracle/agq_oracle.c ora_gemv_ref_f32, reference.rs:53-71), {t_total:.1f} s"}
+
+
+def run_sweep(args, K, B):
+    ctx = Ctx(K, B)
+    cpu_layers = 0 if args.no_cpu else 2
+    t0 = time.time()
+    plan, meta, cpu = build_sweep(ctx, args.m, cpu_layers)
+    print(f"# sweep generated in {time.time() - t0:.1f} s ({len(plan)} launches)", file=sys.stderr, flush=True)
+    arr = (AgbLaunch * len(plan))(*plan)
+    ms = ctypes.c_float()
+    ctx.check(B.agb_run(arr, len(plan), args.warmup, args.steps, 0 if args.eager else 1, ctypes.byref(ms)), "run")
+    total_bytes = sum(algo_bytes(L) for L in plan)
+    gbs = total_bytes / (ms.value * 1e-3) / 1e9
+    # per-launch durations (events around every launch) -> the dominant kernel
+    each = (ctypes.c_float * len(plan))()
+    ctx.check(B.agb_time_each(arr, len(plan), 3, each), "time each")
+    by_kernel = {}
+    for L, (name, b), t in zip(plan, meta, each):
+        key = f"i8_gemv_kernel<{b},128,{(args.m + 3) // 4}>"
+        d = by_kernel.setdefault(key, {"ms": 0.0, "bytes": 0, "launches": 0})
+        d["ms"] += t
+        d["bytes"] += algo_bytes(L)
+        d["launches"] += 1
+    dom_name, dom = max(by_kernel.items(), key=lambda kv: kv[1]["ms"])
+    achieved = dom["bytes"] / (dom["ms"] * 1e-3) / 1e9
+    per_type = {}
+    for L, (name, b), t in zip(plan, meta, each):
+        d = per_type.setdefault(f"{name}_w{b}", {"us": 0.0, "bytes": 0, "n": 0})
+        d["us"] += t * 1e3
+        d["bytes"] += algo_bytes(L)
+        d["n"] += 1
+    detail = {k: {"launches": v["n"], "us_each": round(v["us"] / v["n"], 2),
+                  "GBps": round(v["bytes"] / (v["us"] * 1e-6) / 1e9, 1)} for k, v in sorted(per_type.items())}
+    read_bw = ctypes.c_float()
+    ctx.check(B.agb_read_bw(4 << 30, 5, ctypes.byref(read_bw)), "read bw")
+    cpu_res = cpu_baseline(ctx, args.m, cpu) if cpu else None
+    bits_mix = {f"w{b}": sum(1 for (_, bb) in meta[:-1] if bb == b) // 4 for b in (2, 3, 4)}
+    traffic = None
+    tf = os.path.join(ROOT, "profiles", "traffic_sweep_m1.json")
+    if args.m == 1 and os.path.exists(tf):
+        try:
+            traffic = json.load(open(tf)).get(dom_name)
+        except Exception:
+            traffic = None
+    out = {
+        "metric": "effective HBM GB/s (% of peak) + us per 64-layer 32B decode GEMV sweep, M=1",
+        "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms.value, 4), "us_per_sweep": round(ms.value * 1e3, 1),
+        "pct_of_peak": round(100 * gbs / HBM_PEAK_GBS, 2), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8 MFMA (exact int32 group sums) + fp32 accumulate; bf16 in/out",
+        "data": "synthetic (device-generated int4 container, repacked by ak_wq_repack_kt; random codes/scales/x)",
+        "config": {"workload": "64-layer 32B decode GEMV sweep: QKV 5120->7168 (q/k/v segments), O 5120->5120, "
+                               "gate_up 5120->55296, down 27648->5120, mixed W2/W3/W4 g128 per layer, "
+                               "+ W4 LM head 5120->152064",
+                   "m": args.m, "layers_by_bits": bits_mix, "launches": len(plan),
+                   "bytes_per_sweep": total_bytes, "graph": not args.eager, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "kernel": dom_name, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "launches": dom["launches"], "avg_us": round(dom["ms"] * 1e3 / dom["launches"], 2),
+                     "bytes_per_launch": dom["bytes"] // dom["launches"]},
+        "stream_read_ceiling_GBps": round(read_bw.value, 1),
+        "per_linear": detail,
+        "cpu_baseline": cpu_res,
+    }
+    ctx.free_all()
+    return out
+
+
+def run_single(args, K, B):
+    """one GEMV shape, weights rotated over >= 1 GB of copies (beats the 256 MB cache)."""
+    ctx = Ctx(K, B)
+    cfgs = {0: [(4, [5120], 5120, 1.0)], 1: [(3, [55296], 5120, 1.0)], 2: [(2, [5120], 27648, 0.5)],
+            3: [(4, [5120, 1024, 1024], 5120, 1.0), (4, [5120], 5120, 1.0)]}
+    ms_list = [args.m] if args.config != 3 else [2, 4, 8, 16] if args.m == 1 else [args.m]
+    lines = []
+    for bits, ns, k, xs in cfgs[args.config]:
+        for m in ms_list:
+            one = sum(K.ak_wq_kt_weight_bytes(bits, n, k) + K.ak_w4_kt_scale_bytes(n, k, 128) for n in ns)
+            copies = max(2, (1 << 30) // one + 1)
+            lins = [[QLinear(ctx, SEED + 100 * c + i, n, k, bits) for i, n in enumerate(ns)] for c in range(copies)]
+            x = ctx.alloc(m * k * 2)
+            ctx.check(B.agb_gen_x(SEED + 7, m * k, xs, x, None), "gen x")
+            ys = [ctx.alloc(m * n * 2) for n in ns]
+            plan = [launch(bits, m, k, x, lins[c], ys) for c in range(copies)]
+            arr = (AgbLaunch * len(plan))(*plan)
+            t = ctypes.c_float()
+            steps = max(1, (args.steps * 10 + copies - 1) // copies)
+            ctx.check(B.agb_run(arr, len(plan), args.warmup, steps, 0 if args.eager else 1, ctypes.byref(t)), "run")
+            us = t.value * 1e3 / copies
+            by = algo_bytes(plan[0])
+            lines.append({"config": args.config, "bits": bits, "n": ns, "k": k, "m": m, "us": round(us, 2),
+                          "GBps": round(by / (us * 1e-6) / 1e9, 1), "pct_of_peak": round(100 * by / (us * 1e-6) / 1e9
+                                                                                         / HBM_PEAK_GBS, 2),
+                          "bytes": by, "copies": copies, "graph": not args.eager})
+            ctx.free_all()
+    return lines
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--m", type=int, default=1)
+    ap.add_argument("--config", default="sweep")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--eager", action="store_true")
+    ap.add_argument("--exact", action="store_true", help="the reference's exact fp32 numerics instead")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (the GEMV shards by output rows with no "
+              "communication, or by k with one all-reduce; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        return 2
+    K, B = load_libs()
+    for fn in ("ak_w4_set_lean", "ak_w4_set_mma"):
+        getattr(K, fn).argtypes, getattr(K, fn).restype = [ctypes.c_int], ctypes.c_int
+    if args.exact:
+        K.ak_w4_set_mma(0)
+    name = ctypes.create_string_buffer(128)
+    K.ak_device_name(0, name, 128)
+    print(f"# device {name.value.decode()}", file=sys.stderr, flush=True)
+    if args.config == "sweep":
+        print(json.dumps(run_sweep(args, K, B)), flush=True)
+    else:
+        args.config = int(args.config)
+        for line in run_single(args, K, B):
+            print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

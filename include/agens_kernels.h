@@ -11,7 +11,8 @@
  *     other values are hipError_t codes;
  *   - `stream` is a hipStream_t (NULL = the default stream); launches are asynchronous and stream-ordered;
  *   - bf16 tensors are passed as void* (raw 16-bit patterns), the int4 container as int32_t words;
- *   - the caller owns every buffer it passes; the library owns only per-(device, stream) split-K scratch.
+ *   - the caller owns every buffer it passes; the GEMV entry points allocate nothing (no scratch memory) and never
+ *     synchronize, so they can be captured in a hipGraph.
  */
 #pragma once
 #include <stddef.h>
@@ -111,9 +112,8 @@ int ak_w3_dequant_kt_rows(const void* wt, const void* st, void* w, int n, int k,
 
 /* ---------------------------------------------------------------------------------------------- switches
  * reference: agens_kernels.h:205 / :208 / :211, w4_gemv.cu:3271-3282.  mma: -1 auto (environment AGENS_W4_EXACT), 0 exact
- * fp32 path, 1 default integer-MFMA path.  lean: rb > 0 forces the single-pass variant of the default path (no
- * split-K scratch; same bits), -1 / 0 automatic.  tma selects an sm90-only variant in the reference; accepted and
- * ignored here. */
+ * fp32 path, 1 default integer-MFMA path.  lean / tma select bit-identical sm90-only variants in the reference;
+ * accepted and ignored here (one kernel family per numerics). */
 int ak_w4_set_mma(int mode);
 int ak_w4_set_lean(int rb);
 int ak_w4_set_tma(int stages);

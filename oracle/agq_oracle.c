@@ -300,19 +300,29 @@ static void kt_row_q(int bits, const uint8_t* wt, int n, int k, int o, int8_t* q
     }
 }
 
-static long long group_sum(const uint16_t* xr, const int8_t* q, int k, int g0, int group, int* E) {
+/* Activation limbs of one group: E = largest bf16 exponent field, x_int = trunc(x * 2^(148 - E)) (exact in double),
+ * split into balanced signed bytes x_int = d2 * 2^16 + d1 * 2^8 + d0; returns the three limb sums of d_j * q. */
+static void group_limb_sums(const uint16_t* xr, const int8_t* q, int k, int g0, int group, int* E, long long D[3]) {
   int e = 0;
   for (int i = g0; i < g0 + group; ++i)
     if (i < k && bf16_expf(xr[i]) > e) e = bf16_expf(xr[i]);
-  long long gs = 0;
+  D[0] = D[1] = D[2] = 0;
   for (int i = g0; i < g0 + group; ++i) {
     if (i >= k) continue;
-    const double v = ldexp((double)ora_bf2f(xr[i]), 148 - e);
-    const long long xi = (long long)v; /* truncation toward zero */
-    gs += xi * q[i];
+    const long long xi = (long long)ldexp((double)ora_bf2f(xr[i]), 148 - e); /* truncation toward zero */
+    const long long x1 = (xi + 128) >> 8, x2 = (x1 + 128) >> 8;           /* arithmetic shifts */
+    const long long d0 = xi - x1 * 256, d1 = x1 - x2 * 256, d2 = x2;
+    D[0] += d0 * q[i];
+    D[1] += d1 * q[i];
+    D[2] += d2 * q[i];
   }
   *E = e;
-  return gs;
+}
+
+static long long group_sum(const uint16_t* xr, const int8_t* q, int k, int g0, int group, int* E) {
+  long long D[3];
+  group_limb_sums(xr, q, k, g0, group, E, D);
+  return D[2] * 65536 + D[1] * 256 + D[0];
 }
 
 long long ora_fast_group_sum(int bits, const uint16_t* x, const uint8_t* wt, int n, int k, int group, int o, int g,
@@ -344,10 +354,12 @@ void ora_gemv_fast_kt_rows(int bits, const uint16_t* x, int m, const uint8_t* wt
         for (int s = 0; s < 4; ++s) {
           const int g = 4 * qd + s, t = g * group / 1024, gi = g % SPT;
           int E;
-          const long long GS = group_sum(xr, q, k, g * group, group, &E);
-          const float gs = (float)ldexp((double)GS, E - 148);
-          const float sf = ora_bf2f(st[((size_t)t * n + o) * SPT + gi]);
-          acc[qd % P][s] = fmaf(gs, sf, acc[qd % P][s]);
+          long long D[3];
+          group_limb_sums(xr, q, k, g * group, group, &E, D);
+          const int T = (int)(D[2] * 256 + D[1]);
+          const float gsum = fmaf((float)T, 256.0f, (float)D[0]);
+          const float sE = ora_bf2f(st[((size_t)t * n + o) * SPT + gi]) * ldexpf(1.0f, E - 148);
+          acc[qd % P][s] = fmaf(gsum, sE, acc[qd % P][s]);
         }
       float yv = 0.f;
       for (int p = 0; p < P; ++p) {

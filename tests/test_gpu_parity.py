@@ -230,19 +230,21 @@ def test_large_m_is_chunked_identically():
             K.ak_w4_set_mma(1)
 
 
-def test_single_pass_variant_same_bits():
-    # ak_w4_set_lean(1): the default path without split-K scratch gives the same bits
+def test_long_k_mixed_tokens():
+    # long k (down projection) at every token count of one launch: rows equal the oracle and the m = 1 launches
     K = kernels()
     n, k, g = 700, 27648, 128
     L = make_linear(960, n, k, g, 2)
-    X = Dev.of(gen_x(961, 4 * k))
-    a = y_of(gemv(2, X, 4, [L], k, g)[0], 4, n)
-    K.ak_w4_set_lean(1)
-    try:
-        b = y_of(gemv(2, X, 4, [L], k, g)[0], 4, n)
-    finally:
-        K.ak_w4_set_lean(0)
-    assert (a == b).all()
+    x = gen_x(961, 12 * k)
+    X = Dev.of(x)
+    y = y_of(gemv(2, X, 12, [L], k, g)[0], 12, n)
+    wt, st = L.host_kt()
+    for r0 in (0, n - 64):
+        yo = ora_fast(2, x, 12, wt, st, n, k, g, rows=(r0, r0 + 64))
+        assert (y[:, r0:r0 + 64] == yo[:, r0:r0 + 64]).all()
+    for j in (0, 5, 11):
+        one = y_of(gemv(2, X.addr(j * k * 2), 1, [L], k, g)[0], 1, n)[0]
+        assert (one == y[j]).all()
 
 
 @pytest.mark.parametrize("cfg", [0, 1, 2])
