@@ -88,6 +88,30 @@ __device__ __forceinline__ float group_sum_f32(const i32x4& d) {
 // 2^(E - 148) as fp32 bits (the activation scale of a group whose largest exponent field is E)
 __device__ __forceinline__ int act_scale_bits(int e) { return __float_as_int(ldexpf(1.0f, e - 148)); }
 
+// Reductions over aligned groups of L lanes (L = 2, 4, 8 or 16) with DPP: two quad swaps, then the half-row and the
+// row mirrors (each step pairs every lane with one holding the other half of its group's partial results).
+template <int L, bool MAX>
+__device__ __forceinline__ int dpp_group_reduce(int v) {
+  auto step = [&](int o) { return MAX ? max(v, o) : v + o; };
+  v = step(__builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false));                    // quad_perm [1,0,3,2]
+  if constexpr (L >= 4) v = step(__builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false));  // quad_perm [2,3,0,1]
+  if constexpr (L >= 8) v = step(__builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false)); // row_half_mirror
+  if constexpr (L >= 16) v = step(__builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false)); // row_mirror
+  return v;
+}
+
+// Sum of the signed bytes j of t[0..7] (one limb of eight inputs): packed four at a time, then dot products with ones
+__device__ __forceinline__ int limb_sum8(const uint32_t (&t)[8], int j) {
+  const uint32_t sel = (uint32_t)j | ((uint32_t)(4 + j) << 8) | 0x0C0C0000u;  // [a.byte j, b.byte j, 0, 0]
+  int s = 0;
+#pragma unroll
+  for (int i = 0; i < 8; i += 4) {
+    const uint32_t lo = __builtin_amdgcn_perm(t[i + 1], t[i], sel), hi = __builtin_amdgcn_perm(t[i + 3], t[i + 2], sel);
+    s = __builtin_amdgcn_sdot4((int)(lo | (hi << 16)), 0x01010101, s, false);
+  }
+  return s;
+}
+
 // One group's activation limbs from 8 consecutive bf16 inputs per lane, LPU lanes per group: the group's largest
 // exponent field e (all LPU lanes) and, per input, x_int = trunc(x * 2^(148 - e)) with its three limb-byte sources.
 template <int LPU>
@@ -96,8 +120,7 @@ __device__ __forceinline__ int group_limbs(const uint4 v, uint32_t (&t0)[8], uin
   int e = 0;
 #pragma unroll
   for (int i = 0; i < 4; ++i) e = max(e, max((int)((w[i] >> 7) & 0xFFu), (int)((w[i] >> 23) & 0xFFu)));
-#pragma unroll
-  for (int o = 1; o < LPU; o <<= 1) e = max(e, __shfl_xor(e, o));
+  e = dpp_group_reduce<LPU, true>(e);
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const uint32_t b16 = (w[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;

@@ -16,6 +16,12 @@
 #include "wq_common.h"
 #include "wq_i8_common.h"
 
+// phase timestamps for profiling builds (a build that defines it records them; product builds compile nothing)
+#ifndef AK_M1_STAMP
+#define AK_M1_STAMP(i)
+#define AK_M1_STAMP_AFTER(i, v)
+#endif
+
 namespace agq {
 
 int num_cus();
@@ -24,7 +30,7 @@ namespace {
 
 struct ItemPos {
   int it, ls, qd;
-  bool valid;
+  int valid;  // an int, not a bool: a padded struct is copied through scratch memory
 };
 
 template <int BITS, int G, int SWD, int NWV, int WPE>
@@ -34,18 +40,18 @@ __global__ void __launch_bounds__(64 * NWV, WPE) i8_m1_kernel(const I8Args a) {
   constexpr int RWV = NWV / SWD;             // row blocks per workgroup iteration
   constexpr int NPW = (8 + SWD - 1) / SWD;   // most stripes of one wave
   const int P = a.P, nquad = a.nquad, k = a.k;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: keeps the item bookkeeping scalar
   const int sw = wave % SWD, rw = wave / SWD;
   const int r = lane & 15, h = lane >> 4;
   const Segs& sgs = a.segs;
   const int rows_pad = sgs.end[sgs.nseg - 1];
   const int n_rb = rows_pad >> 4;
 
-  // LDS: zeros [512 B] | limbs [nquad][CPQ][2][3][16 B] | meta [nquad][4] int4 | E [nquad][4] | partials | tickets
+  // LDS: zeros [512 B] | limbs [nquad][CPQ][2][3][16 B] | meta [nquad][4] int4 | partials | tickets
   uint8_t* xq = lds + 512;
   i32x4* meta = reinterpret_cast<i32x4*>(xq + nquad * CPQ * 96);
-  int* ex = reinterpret_cast<int*>(meta + nquad * 4);
-  float* part = reinterpret_cast<float*>(ex + nquad * 4);  // [iters_max][RWV][8][16]
+  float* part = reinterpret_cast<float*>(meta + nquad * 4);  // [iters_max][RWV][8][16]
   int* tickets = reinterpret_cast<int*>(part + (SWD > 1 ? a.iters_max * RWV * 8 * 16 : 0));
 
   auto row_info = [&](int rb, const void*& wt, const uint16_t*& st, int& n, int& orow, bool& ok) {
@@ -77,12 +83,13 @@ __global__ void __launch_bounds__(64 * NWV, WPE) i8_m1_kernel(const I8Args a) {
     }
   };
   auto fetch = [&](const ItemPos& x, Raw<BITS>(&dst)[CPG], uint32_t& sdst) {
-    if (!x.valid) return;
+    // branch-free: an invalid item (past the end) loads row block 0 (L2-resident, never used), so the compiler keeps
+    // exact load counters across the fetches instead of draining every outstanding load at a control-flow merge
     const void* wt;
     const uint16_t* st;
     int n, orow;
     bool ok;
-    row_info(x.it * RWV + rw, wt, st, n, orow, ok);
+    row_info(x.valid ? x.it * RWV + rw : 0, wt, st, n, orow, ok);
     const int cg0 = x.qd * CPQ + h * CPG;  // this lane group's group: chunks cg0 .. cg0 + CPG - 1 (one tile)
     const size_t rec = (size_t)(cg0 >> 5) * n + orow;
 #pragma unroll
@@ -95,7 +102,35 @@ __global__ void __launch_bounds__(64 * NWV, WPE) i8_m1_kernel(const I8Args a) {
     for (int i = tid; i < a.iters_max * RWV; i += 64 * NWV) tickets[i] = 0;
   if (tid < 128) reinterpret_cast<uint32_t*>(lds)[tid] = 0u;
 
-  // the first two items are requested before the activations are converted (weights do not depend on them)
+  // ---- activations, step 1: every lane's bf16 inputs are requested first (x is small and mostly L2-resident), then
+  // the first two weight items, so that waiting for x does not wait for the weights.
+  constexpr int UPW = 64 / LPU, XB = 8;  // groups per wave and pass, passes per load batch
+  const int sub = lane % LPU, units = nquad * 4, ustride = NWV * UPW;
+  const int u0 = wave * UPW + lane / LPU;
+  const int npass = (units + ustride - 1) / ustride;
+  uint4 xv[XB];
+  auto xload = [&](int pass0) {
+#pragma unroll
+    for (int b = 0; b < XB; ++b) {
+      // unconditional loads (clamped address, zero-selected) keep the load sequence branch-free
+      // lanes past the end load x[0] (zero-selected); passes past npass load nothing (a wave-uniform branch)
+      const int u = u0 + (pass0 + b) * ustride, kk = u * G + 8 * sub;
+      const bool ok = u < units && kk < k;
+      xv[b] = make_uint4(0u, 0u, 0u, 0u);
+      if (pass0 + b < npass) {
+        const uint4 v = *reinterpret_cast<const uint4*>(a.x + (ok ? kk : 0));
+        xv[b] = ok ? v : make_uint4(0u, 0u, 0u, 0u);
+      }
+    }
+  };
+  AK_M1_STAMP(0);
+  xload(0);
+  AK_M1_STAMP_AFTER(1, lane);
+  // wait for x before requesting weights: behind the weight requests of the whole GPU, x (one cache line per XCD to
+  // miss) would arrive microseconds late
+#pragma unroll
+  for (int b = 0; b < XB; ++b) asm volatile("" ::"v"(xv[b].x), "v"(xv[b].y), "v"(xv[b].z), "v"(xv[b].w));
+
   ItemPos pa = first(), pb = pa;
   advance(pb);
   pb.valid = pb.valid && pa.valid;
@@ -104,30 +139,38 @@ __global__ void __launch_bounds__(64 * NWV, WPE) i8_m1_kernel(const I8Args a) {
   fetch(pa, buf0, s0);
   fetch(pb, buf1, s1);
 
-  // ---- activations: limbs and E of every group, all quads
-  {
-    const int sub = lane % LPU, units = nquad * 4;
-    for (int base = wave * (64 / LPU); base < units; base += NWV * (64 / LPU)) {
-      const int u = base + lane / LPU;
-      const bool live = u < units;
-      const int qd = live ? u >> 2 : 0, gq = u & 3;
-      const int kk = (qd * 4 + gq) * G + 8 * sub;
-      uint4 v = make_uint4(0u, 0u, 0u, 0u);
-      if (live && kk < k) v = *reinterpret_cast<const uint4*>(a.x + kk);
+  // ---- activations, step 2: per group the limbs (to LDS), and in meta the bias sums -OFF * sum(d_j) of the three
+  // limbs with the activation scale 2^(E - 148) as float bits
+  auto convert = [&](int p0) {
+    AK_M1_STAMP_AFTER(2, xv[0].x);
+#pragma unroll
+    for (int b = 0; b < XB; ++b) {
+      if (p0 + b >= npass) break;
+      const int u = u0 + (p0 + b) * ustride;
       uint32_t t0[8], t1[8], t2[8];
-      const int e = group_limbs<LPU>(v, t0, t1, t2);
-      if (live) {
-        const int eg0 = 8 * sub, cq = gq * CPG + (eg0 >> 5);
+      const int e = group_limbs<LPU>(xv[b], t0, t1, t2);
+      const int b0 = dpp_group_reduce<LPU, false>(limb_sum8(t0, 0));
+      const int b1 = dpp_group_reduce<LPU, false>(limb_sum8(t1, 1));
+      const int b2 = dpp_group_reduce<LPU, false>(limb_sum8(t2, 2));
+      if (u < units) {
+        const int qd = u >> 2, gq = u & 3, eg0 = 8 * sub, cq = gq * CPG + (eg0 >> 5);
         store_limbs<BITS>(xq + (qd * CPQ + cq) * 96, 48, eg0 & 31, t0, t1, t2);
-        if (sub == 0) ex[qd * 4 + gq] = e;
+        if (sub == 0) {
+          constexpr int OFF = code_offset<BITS>();
+          const i32x4 mv = {-OFF * b0, -OFF * b1, -OFF * b2, act_scale_bits(e)};
+          meta[u] = mv;
+        }
       }
     }
+  };
+  convert(0);
+  for (int p0 = XB; p0 < npass; p0 += XB) {
+    xload(p0);
+    convert(p0);
   }
   __syncthreads();
-  // ---- bias sums -OFF * sum(d_j) of every group (MFMA against the constant -OFF operand) and the activation scales
   const int limb_a = r & 3, ua = r >> 2;
   const bool a_on = limb_a < 3 && ua == h;  // A row 4u + j is fed only by lane group u
-  const i32x4 zero = {0, 0, 0, 0};
   // branch-free A reads: inactive lanes read the zeroed region at the start of the LDS (quad offset forced to 0)
   const int a_base = a_on ? 512 + (h * CPG * 96 + 16 * limb_a) : 0;
   const int a_qmul = a_on ? CPQ * 96 : 0;
@@ -136,25 +179,6 @@ __global__ void __launch_bounds__(64 * NWV, WPE) i8_m1_kernel(const I8Args a) {
     a0 = *reinterpret_cast<const i32x4*>(src);
     a1 = *reinterpret_cast<const i32x4*>(src + 48);
   };
-  {
-    const i32x4 negoff = {neg_off_bytes<BITS>(), neg_off_bytes<BITS>(), neg_off_bytes<BITS>(), neg_off_bytes<BITS>()};
-    for (int qd = wave; qd < nquad; qd += NWV) {
-      i32x4 d = zero;
-#pragma unroll
-      for (int s = 0; s < CPG; ++s) {
-        i32x4 a0, a1;
-        a_read(qd, s, a0, a1);
-        d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, negoff, d, 0, 0, 0);
-        d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, negoff, d, 0, 0, 0);
-      }
-      if (r == 0) {
-        i32x4 v = d;
-        v[3] = act_scale_bits(ex[qd * 4 + h]);
-        meta[qd * 4 + h] = v;
-      }
-    }
-  }
-  __syncthreads();
 
   // ---- items
   float acc = 0.f;
@@ -245,15 +269,22 @@ __global__ void __launch_bounds__(64 * NWV, WPE) i8_m1_kernel(const I8Args a) {
     advance(pc);
     pc.valid = pc.valid && pa.valid;
   }
+  AK_M1_STAMP(3);
+}
+
+template <int G>
+size_t m1_x_bytes(int nquad) {
+  constexpr int CPQ = 4 * G / 32;
+  return 512 + (size_t)nquad * (CPQ * 96 + 4 * 16);  // zeros, limbs, meta
 }
 
 template <int BITS, int G, int SWD, int NWV>
 int launch_m1(I8Args a, hipStream_t s) {
-  constexpr int RWV = NWV / SWD, CPQ = 4 * G / 32;
+  constexpr int RWV = NWV / SWD;
   const int rows_pad = a.segs.end[a.segs.nseg - 1];
   const int n_rb = rows_pad / 16;
   const int n_iter = (n_rb + RWV - 1) / RWV;
-  const size_t x_bytes = 512 + (size_t)a.nquad * (CPQ * 96 + 4 * 16 + 4 * 4);
+  const size_t x_bytes = m1_x_bytes<G>(a.nquad);
   // workgroups per CU: LDS (160 KB per CU) and waves (NWV each; up to 4 waves per SIMD at <= 128 VGPRs)
   int per_cu = (int)((160 * 1024) / (x_bytes + 4096));
   const int by_waves = 16 / NWV;
@@ -268,25 +299,38 @@ int launch_m1(I8Args a, hipStream_t s) {
   return (int)hipGetLastError();
 }
 
-template <int BITS, int G>
-int m1_shape(const I8Args& a, hipStream_t s) {
+template <int BITS, int G, int NWV>
+int m1_swd(const I8Args& a, hipStream_t s) {
   // enough waves to cover the GPU: each row block is shared by SWD stripe-waves (SWD <= P, a power of 2)
   const int n_rb = a.segs.end[a.segs.nseg - 1] / 16;
-  const int target = num_cus() * 8;
+  const int target = num_cus() * NWV;
   int swd = 1;
   while (swd < 8 && swd * 2 <= a.P && n_rb * swd < target) swd *= 2;
   switch (swd) {
-    case 1: return launch_m1<BITS, G, 1, 8>(a, s);
-    case 2: return launch_m1<BITS, G, 2, 8>(a, s);
-    case 4: return launch_m1<BITS, G, 4, 8>(a, s);
-    default: return launch_m1<BITS, G, 8, 8>(a, s);
+    case 1: return launch_m1<BITS, G, 1, NWV>(a, s);
+    case 2: return launch_m1<BITS, G, 2, NWV>(a, s);
+    case 4: return launch_m1<BITS, G, 4, NWV>(a, s);
+    default: return launch_m1<BITS, G, 8, NWV>(a, s);
   }
+}
+
+template <int BITS, int G>
+int m1_shape(const I8Args& a, hipStream_t s) {
+  // one 16-wave workgroup per CU when two copies of x would fit the LDS (x is converted once per CU, not twice)
+  if ((160 * 1024) / (m1_x_bytes<G>(a.nquad) + 4096) >= 2) return m1_swd<BITS, G, 16>(a, s);
+  return m1_swd<BITS, G, 8>(a, s);
 }
 
 }  // namespace
 
 // one token; segments padded to 16 rows.  Returns 1 if the activation vector does not fit the LDS (caller falls back).
+int i8_gemv_m1d(int bits, const void* x, const Segs& g, int k, hipStream_t s);
+
 int i8_gemv_m1(int bits, const void* x, const Segs& g, int k, int group, hipStream_t s) {
+  if (group == 128) {
+    const int e = i8_gemv_m1d(bits, x, g, k, s);
+    if (e != AK_INVALID) return e;
+  }
   I8Args a;
   a.segs = g;
   a.x = static_cast<const uint16_t*>(x);
