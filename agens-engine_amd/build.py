@@ -16,7 +16,7 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libagens_kernels.so")
 BENCH_LIB = os.path.join(HERE, "libagens_bench.so")
-SOURCES = ["ak_runtime.hip", "wq_layout.hip", "wq_exact.hip", "wq_i8.hip", "wq_i8m1.hip", "wq_i8m1d.hip", "wq_api.hip"]
+SOURCES = ["ak_runtime.hip", "wq_layout.hip", "wq_exact.hip", "wq_i8.hip", "wq_i8m1d.hip", "wq_api.hip"]
 
 
 def hipcc():

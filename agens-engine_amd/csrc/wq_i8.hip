@@ -12,8 +12,9 @@
 //     sum(d_j * n) - OFF * sum(d_j) (the second term from the same activation operand against a constant -OFF
 //     operand), i.e. the exact integer limb sums of sum(d_j * q); GS = combined exactly in fp64;
 //     gs = fp32_rn(GS * 2^(E - 148));
-//   groups are taken in quads (4 consecutive groups, slot s = g % 4) and quads in P = min(8, #quads) stripes
-//     (stripe = quad % P); acc[p][s] = fmaf(gs, scale, acc[p][s]) over a stripe's quads in order;
+//   groups are taken in quads (4 consecutive groups, slot s = g % 4) and quads in P = min(8, #quads) contiguous
+//     stripes (stripe p = quads [p * nquad / P, (p + 1) * nquad / P)); acc[p][s] = fmaf(gs, scale, acc[p][s]) over a
+//     stripe's quads in order;
 //     part[p] = ((acc[p][0] + acc[p][1]) + acc[p][2]) + acc[p][3]; y = part[0] + part[1] + ... left to right; bf16 RN.
 // The group sums are exact, so every kernel shape (token count, segmentation, row grouping, bit width of the same
 // values) gives the same bits; only the fixed fp32 order above rounds.
@@ -43,7 +44,7 @@ namespace {
 // LDS layout of a stripe-wave's activation batch:
 //   xl[(((qi * CPQ + cq) * 2 + half) * m + token) * 48 + limb * 16 + 4v + b]   (three 16-byte limb rows per token)
 //   ex[(qi * 4 + gq) * m + token] = E
-// Converts the units (quad qi, group gq, token j) of quads p + (i0 + qi) * P, qi < nbq; the RW waves of this stripe
+// Converts the units (quad qi, group gq, token j) of quads stripe_begin(p) + i0 + qi, qi < nbq; the RW waves of this stripe
 // share the work: the LPU = G / 8 lanes of a unit hold 8 consecutive inputs each.
 template <int BITS, int G, int RW>
 __device__ __forceinline__ void convert_batch(const I8Args& a, int p, int i0, int nbq, int rw, uint8_t* xl, int* ex) {
@@ -54,7 +55,7 @@ __device__ __forceinline__ void convert_batch(const I8Args& a, int p, int i0, in
     const int u = base + lane / LPU;
     const bool live = u < units;
     const int qi = live ? u / (4 * m) : 0, rem = live ? u % (4 * m) : 0, gq = rem / m, j = rem % m;
-    const int kk = ((p + (i0 + qi) * a.P) * 4 + gq) * G + 8 * sub;
+    const int kk = ((stripe_begin(p, a.nquad, a.P) + i0 + qi) * 4 + gq) * G + 8 * sub;
     uint4 v = make_uint4(0u, 0u, 0u, 0u);
     if (live && kk < k) v = *reinterpret_cast<const uint4*>(a.x + (size_t)j * k + kk);
     uint32_t t0[8], t1[8], t2[8];
@@ -159,8 +160,9 @@ __global__ void __launch_bounds__(64 * SW * RW, WPE) i8_gemv_kernel(const I8Args
 
   for (int p0 = 0; p0 < P; p0 += SW) {
     const int p = p0 + sw;
-    const int nq = p < P ? (a.nquad - p + P - 1) / P : 0;
-    const int nq_round = (a.nquad - p0 + P - 1) / P;  // stripe p0 has the most quads
+    const int q0 = p < P ? stripe_begin(p, a.nquad, P) : 0;
+    const int nq = p < P ? stripe_begin(p + 1, a.nquad, P) - q0 : 0;
+    const int nq_round = (a.nquad + P - 1) / P;  // no stripe has more quads
     for (int i0 = 0; i0 < nq_round; i0 += nb) {
       const int nbq = nq - i0 < nb ? nq - i0 : nb;  // <= 0 when this wave's stripe has no quad here
       const bool last_batch = i0 + nb >= nq;
@@ -169,7 +171,7 @@ __global__ void __launch_bounds__(64 * SW * RW, WPE) i8_gemv_kernel(const I8Args
         if (t >= T) return;
         const int j = t / nbq, qi = t - j * nbq;
         const RowBlock b = row_block(sgs, rb0 + j, r, rows_pad);
-        const int qd = p + (i0 + qi) * P;
+        const int qd = q0 + i0 + qi;
 #pragma unroll
         for (int s = 0; s < SPQ; ++s) {
           const int cg = qd * CPQ + 4 * s + h;

@@ -11,8 +11,11 @@ struct I8Args {
   int m, k;
   int nquad, P;   // quads of the padded k, stripes
   int nb;         // quads per LDS batch (any-m kernel)
-  int iters_max;  // row-block iterations per workgroup (m = 1 kernel)
+  int wg_end[4];  // m = 1 kernel: workgroups of segments 0..i (each workgroup serves one segment)
 };
+
+// first quad of stripe p: the P stripes are contiguous runs of quads, stripe p = [p * nquad / P, (p + 1) * nquad / P)
+__host__ __device__ inline int stripe_begin(int p, int nquad, int P) { return p * nquad / P; }
 
 namespace {
 
@@ -67,14 +70,18 @@ __device__ __forceinline__ void make_b(const Raw<BITS>& r, i32x4& b0, i32x4& b1)
     }
   } else {
     const uint32_t L0 = r.lo.x, L1 = r.lo.y, H = r.hi;
-    // bytes m of P0 / P1 hold the 2-bit fields of inputs 8m .. 8m+3 / 8m+4 .. 8m+7
-    const uint32_t P0 = (L0 & 0xFFu) | ((L0 >> 8) & 0xFF00u) | ((L1 & 0xFFu) << 16) | ((L1 << 8) & 0xFF000000u);
-    const uint32_t P1 = ((L0 >> 8) & 0xFFu) | ((L0 >> 16) & 0xFF00u) | ((L1 << 8) & 0xFF0000u) | (L1 & 0xFF000000u);
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      b0[t] = (int)(((P0 >> (2 * t)) & 0x03030303u) | (((H >> t) & 0x01010101u) << 2));
-      b1[t] = (int)(((P1 >> (2 * t)) & 0x03030303u) | (((H >> (t + 4)) & 0x01010101u) << 2));
-    }
+    // bytes m of P0 / P1 hold the 2-bit fields of inputs 8m .. 8m+3 / 8m+4 .. 8m+7 (bytes 0, 2 / 1, 3 of L0 and L1)
+    const uint32_t P0 = __builtin_amdgcn_perm(L1, L0, 0x06040200u), P1 = __builtin_amdgcn_perm(L1, L0, 0x07050301u);
+    // code byte = 2-bit field | third bit << 2; the third bits of inputs 8m + t sit in bit t of byte m of H, moved to
+    // bit 2 with one shift and one mask, then merged by one and-or (31 operations per lane chunk)
+    b0[0] = (int)((P0 & 0x03030303u) | ((H << 2) & 0x04040404u));
+    b0[1] = (int)(((P0 >> 2) & 0x03030303u) | ((H << 1) & 0x04040404u));
+    b0[2] = (int)(((P0 >> 4) & 0x03030303u) | (H & 0x04040404u));
+    b0[3] = (int)(((P0 >> 6) & 0x03030303u) | ((H >> 1) & 0x04040404u));
+    b1[0] = (int)((P1 & 0x03030303u) | ((H >> 2) & 0x04040404u));
+    b1[1] = (int)(((P1 >> 2) & 0x03030303u) | ((H >> 3) & 0x04040404u));
+    b1[2] = (int)(((P1 >> 4) & 0x03030303u) | ((H >> 4) & 0x04040404u));
+    b1[3] = (int)(((P1 >> 6) & 0x03030303u) | ((H >> 5) & 0x04040404u));
   }
 }
 

@@ -16,16 +16,28 @@
 // the A operand has 12 useful rows instead of 3, and row blocks are 4 rows, so work divides evenly over 256 CUs for
 // the decode shapes.
 //
-// Work decomposition: one persistent workgroup per CU owns a contiguous range of 4-row blocks.  Its tasks are
-// (block, stripe set j < SPLIT) pairs, dealt round-robin to the waves; a task runs the stripes j, j + SPLIT, ... of
-// its block one after the other, each over the quads p, p + P, ... (the fp32 order of the numerics).  With SPLIT = 1 a
-// wave owns whole blocks and adds the stripe partials itself; otherwise the partials meet in LDS and the last task of
-// a block to finish (LDS ticket) adds them in stripe order.  Every wave streams its items (one quad of one block: one
-// buffer load per lane, two for W3, plus one for the scales) through DEPTH register buffers; each item's offsets are
-// wave-uniform (scalar registers) on top of per-lane offsets fixed for the task.
+// Work decomposition: one persistent workgroup per CU owns a contiguous range of 4-row blocks of one segment.  Its
+// tasks are (block, stripe set j < SPLIT) pairs: stripe set j = the contiguous stripes [j P / SPLIT, (j + 1) P / SPLIT),
+// i.e. a contiguous run of quads, walked in order (the fp32 order of the numerics).  Wave w always takes stripe set
+// w % SPLIT, for the blocks w / SPLIT, w / SPLIT + nwv / SPLIT, ...  With SPLIT = 1 a wave owns whole blocks and adds
+// the stripe partials itself; otherwise the partials meet in LDS and the last task of a block to finish (LDS ticket)
+// adds them in stripe order.
+//
+// Item pipeline: every wave streams its items (one quad of one block: one buffer load per lane, two for W3, plus one
+// for the scales) through DEPTH register buffers.  A group of DEPTH items is one branch-free block of code, so the
+// compiler interleaves the unpacking, LDS reads and MFMAs of neighbouring items: the load offsets are a fixed per-lane
+// part plus a scalar part of (block, quad), the cursors advance by selects, and a stripe that ends inside the group
+// only leaves a copy of its accumulators; the group's epilogue turns those into stripe partials.
 #include "agens_kernels.h"
 #include "wq_common.h"
 #include "wq_i8_common.h"
+
+// phase timestamps for profiling builds (a build that defines them records them; product builds compile nothing)
+#ifndef AK_M1_STAMP
+#define AK_M1_STAMP(i)
+#define AK_M1_STAMP_AFTER(i, v)
+#define AK_M1_STAMP_ITEM(i)
+#endif
 
 namespace agq {
 
@@ -52,18 +64,11 @@ __device__ __forceinline__ T pick4(int i, T v0, T v1, T v2, T v3) {
 #define AK_PICK(i, arr) pick4((i), (arr)[0], (arr)[1], (arr)[2], (arr)[3])
 static_assert(kMaxSegs == 4, "segment selects cover four segments");
 
-// a wave's position in its task list
-struct Cursor {
-  int t;   // task, local to the workgroup
-  int b;   // block, local to the workgroup
-  int p;   // stripe
-  int qd;  // quad
-};
-
-template <int BITS, int SPLIT, int DEPTH>
+template <int BITS, int SPLIT, int DEPTH, int RB>
 __global__ void __launch_bounds__(1024, 1) i8_m1d_kernel(const I8Args a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   constexpr int LPU = kG / 8, UPW = 64 / LPU, XB = 4;
+  constexpr int REC = Rec<BITS>::bytes, CHB = Rec<BITS>::chunk;
   const int P = a.P, nquad = a.nquad, k = a.k;
   const int nwv = blockDim.x >> 6;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -71,10 +76,16 @@ __global__ void __launch_bounds__(1024, 1) i8_m1d_kernel(const I8Args a) {
   const int c = lane & 15, h = lane >> 4;
   const int rr = c >> 2, vv = c & 3;  // B role: row of the block, group of the quad
   const Segs& sgs = a.segs;
-  const int n_b4 = sgs.end[sgs.nseg - 1] >> 2;
-  const int b_lo = (int)((long long)blockIdx.x * n_b4 / gridDim.x);
-  const int nb = (int)((long long)(blockIdx.x + 1) * n_b4 / gridDim.x) - b_lo;
-  const int ntask = nb * SPLIT;
+
+  // this workgroup's segment and its blocks [b_lo, b_lo + nb) of that segment
+  int sg = 0;
+#pragma unroll
+  for (int i = 1; i < kMaxSegs; ++i) sg += (i < sgs.nseg && (int)blockIdx.x >= a.wg_end[i - 1]) ? 1 : 0;
+  const int wg0 = sg ? AK_PICK(sg - 1, a.wg_end) : 0, gs = AK_PICK(sg, a.wg_end) - wg0, w = blockIdx.x - wg0;
+  const int n = AK_PICK(sg, sgs.n), n_b4 = (n + 3) >> 2;
+  const int b_lo = (int)((long long)w * n_b4 / gs);
+  const int nb = (int)((long long)(w + 1) * n_b4 / gs) - b_lo;
+  uint16_t* const yseg = AK_PICK(sg, sgs.y);
 
   // LDS: zeros [512 B] | limbs [nquad][16][2][3][16 B] | meta [nquad][4] int4 | outputs [nb][4] bf16 |
   //      partials [nb][P][4] | tickets [nb]
@@ -97,6 +108,7 @@ __global__ void __launch_bounds__(1024, 1) i8_m1d_kernel(const I8Args a) {
   auto xload = [&](int pass0) {
 #pragma unroll
     for (int b = 0; b < XB; ++b) {
+      // lanes past the end load x[0] (zero-selected); passes past npass load nothing (a wave-uniform branch)
       const int u = u0 + (pass0 + b) * ustride, kk = u * kG + 8 * sub;
       const bool ok = u < units && kk < k;
       xv[b] = make_uint4(0u, 0u, 0u, 0u);
@@ -106,89 +118,75 @@ __global__ void __launch_bounds__(1024, 1) i8_m1d_kernel(const I8Args a) {
       }
     }
   };
+  AK_M1_STAMP(0);
   xload(0);
 #pragma unroll
   for (int b = 0; b < XB; ++b) asm volatile("" ::"v"(xv[b].x), "v"(xv[b].y), "v"(xv[b].z), "v"(xv[b].w));
+  AK_M1_STAMP(1);
 
-  // ---- task walk.  Task t: block t / SPLIT, stripe set t % SPLIT; a wave takes tasks wave, wave + nwv, ...
-  auto start = [&](Cursor& x, int t) {
-    x.t = t;
-    x.b = t / SPLIT;
-    x.p = t % SPLIT;
-    x.qd = x.p;
-  };
-  auto advance = [&](Cursor& x) {
-    x.qd += P;
-    if (x.qd >= nquad) {
-      x.p += SPLIT;
-      if (x.p >= P) {
-        start(x, x.t + nwv);
-      } else {
-        x.qd = x.p;
-      }
-    }
-  };
-  // items of this wave
-  int nitems = 0;
-  for (int t = wave; t < ntask; t += nwv)
-    for (int p = t % SPLIT; p < P; p += SPLIT) nitems += (nquad - p + P - 1) / P;
+  // ---- this wave's tasks: stripe set j, quads [qa, qb), block groups b0w, b0w + bstep, ... < ng (a group is RB
+  // consecutive blocks: an item loads the same quad of each, and they share its activation operand)
+  const int ng = (nb + RB - 1) / RB;
+  const int j = wave % SPLIT, bstep = nwv / SPLIT, b0w = wave / SPLIT;
+  const int pa = j * P / SPLIT, pb = (j + 1) * P / SPLIT;
+  const int qa = stripe_begin(pa, nquad, P), qb = stripe_begin(pb, nquad, P);
+  const int ntw = b0w < ng ? (ng - b0w + bstep - 1) / bstep : 0;
+  const int nitems = ntw * (qb - qa);
+  // bit q - qa set when quad q is the last of its stripe (quads < qa + 128)
+  unsigned long long ends0 = 0, ends1 = 0;
+  for (int p = pa; p < pb; ++p) {
+    const int r = stripe_begin(p + 1, nquad, P) - 1 - qa;
+    if (r < 64) ends0 |= 1ull << r;
+    else ends1 |= 1ull << (r - 64);
+  }
 
-  // per-task buffer addressing of the fetch cursor: resources of the block's segment and this lane's offsets
-  struct Addr {
-    __amdgpu_buffer_rsrc_t w, s;
-    int vo_w, vo_h, vo_s;  // per lane: weights (W3: two-bit planes), W3 third-bit plane, scale dword
-    int tile_w, tile_s;    // bytes between 1024-input tiles of the segment (n records / n scale rows)
-  };
+  // ---- weight addressing: per lane fixed, per item scalar.  Rows past the segment's end (padding of the last block)
+  // read other rows or, past the buffer, zeros; their results are not written.
   const int tiles = kpad(k) >> 10;
-  auto address = [&](int bl, Addr& ad) {
-    const int g0 = (b_lo + (bl < nb ? bl : 0)) * 4;
-    const int sg = seg_of(sgs, g0);
-    const int n = AK_PICK(sg, sgs.n);
-    int orow = g0 - (sg ? AK_PICK(sg - 1, sgs.end) : 0) + rr;
-    if (orow >= n) orow = 0;  // padding rows read row 0 (results unused)
-    ad.w = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(AK_PICK(sg, sgs.wt)), (short)0,
-                                             tiles * n * Rec<BITS>::bytes, kRsrcWord3);
-    ad.s = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(AK_PICK(sg, sgs.st)), (short)0, tiles * n * 16,
-                                             kRsrcWord3);
-    const int ch = 4 * vv + h;  // this lane's chunk within the 16 of a quad
-    ad.vo_w = orow * Rec<BITS>::bytes + ch * Rec<BITS>::chunk;
-    ad.vo_h = orow * Rec<BITS>::bytes + 256 + ch * 4;
-    ad.vo_s = orow * 16 + (vv & 2) * 2;
-    ad.tile_w = n * Rec<BITS>::bytes;
-    ad.tile_s = n * 16;
-  };
-  // one item: its weights and the dword holding its scale (an item past the end reloads quad 0: cache-resident, never
-  // used, and it keeps the load sequence branch-free so the compiler's load counters stay exact)
-  auto fetch = [&](const Cursor& x, const Addr& ad, Raw<BITS>& dst, uint32_t& sdst) {
-    const int qd = x.t < ntask ? x.qd : 0;
-    const int so = (qd >> 1) * ad.tile_w, odd = qd & 1;
+  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<void*>(AK_PICK(sg, sgs.wt)), (short)0, tiles * n * REC, kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(AK_PICK(sg, sgs.st)), (short)0, tiles * n * 16, kRsrcWord3);
+  const int ch = 4 * vv + h;  // this lane's chunk within the 16 of a quad
+  const int vo_w = rr * REC + ch * CHB, vo_h = rr * REC + 256 + ch * 4, vo_s = rr * 16 + (vv & 2) * 2;
+  const int tile_w = n * REC, tile_s = n * 16;
+  auto fetch1 = [&](int blk, int qd, Raw<BITS>& dst, uint32_t& sdst) {
+    const int row0 = (b_lo + blk) * 4;
+    const int so = row0 * REC + (qd >> 1) * tile_w, odd = qd & 1;
     if constexpr (BITS == 4) {
-      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(ad.w, ad.vo_w, so + odd * 256, kNt);
+      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rw, vo_w, so + odd * 256, kNt);
       dst.w = make_uint4(v[0], v[1], v[2], v[3]);
     } else {
       typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-      const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(ad.w, ad.vo_w, so + odd * 128, kNt);
+      const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rw, vo_w, so + odd * 128, kNt);
       dst.lo = make_uint2(v[0], v[1]);
-      if constexpr (BITS == 3) dst.hi = __builtin_amdgcn_raw_buffer_load_b32(ad.w, ad.vo_h, so + odd * 64, kNt);
+      if constexpr (BITS == 3) dst.hi = __builtin_amdgcn_raw_buffer_load_b32(rw, vo_h, so + odd * 64, kNt);
     }
-    sdst = __builtin_amdgcn_raw_buffer_load_b32(ad.s, ad.vo_s, (qd >> 1) * ad.tile_s + odd * 8, 0);
+    // the aligned dword holding the scale (the item selects its half): a 16-bit value would be widened or packed at
+    // the loop latch, which waits for the load
+    sdst = __builtin_amdgcn_raw_buffer_load_b32(rs, vo_s, row0 * 16 + (qd >> 1) * tile_s + odd * 8, 0);
+  };
+  auto fetch = [&](int grp, int qd, Raw<BITS> (&dst)[RB], uint32_t (&sdst)[RB]) {
+#pragma unroll
+    for (int r = 0; r < RB; ++r) fetch1(grp * RB + r, qd, dst[r], sdst[r]);
   };
 
-  Raw<BITS> buf[DEPTH];
-  uint32_t sbuf[DEPTH];
+  Raw<BITS> buf[DEPTH][RB];
+  uint32_t sbuf[DEPTH][RB];
+
+  // fetch cursor (an item past the end reloads quad qa of block 0: cache-resident, never used, and the load sequence
+  // stays branch-free so the compiler's load counters stay exact)
+  int fb = b0w, fq = qa;
+  auto fetch_next = [&](Raw<BITS> (&dst)[RB], uint32_t (&sdst)[RB]) {
+    const bool in = fb < ng;
+    fetch(in ? fb : 0, in ? fq : qa, dst, sdst);
+    const bool wrap = fq + 1 == qb;
+    fq = wrap ? qa : fq + 1;
+    fb = wrap ? fb + bstep : fb;
+  };
 
   // ---- the first DEPTH items are requested, then step 2 of the activations: per group the limbs (to LDS), and in
   // meta the bias sums -OFF * sum(d_j) of the three limbs with the activation scale 2^(E - 148) as float bits
-  Cursor fc;
-  start(fc, wave);
-  Addr fa;
-  address(fc.b, fa);
-  auto fetch_next = [&](Raw<BITS>& dst, uint32_t& sdst) {
-    fetch(fc, fa, dst, sdst);
-    const int t0 = fc.t;
-    advance(fc);
-    if (fc.t != t0) address(fc.b, fa);
-  };
 #pragma unroll
   for (int d = 0; d < DEPTH; ++d) fetch_next(buf[d], sbuf[d]);
 
@@ -203,8 +201,8 @@ __global__ void __launch_bounds__(1024, 1) i8_m1d_kernel(const I8Args a) {
       const int b1 = dpp_group_reduce<LPU, false>(limb_sum8(t1, 1));
       const int b2 = dpp_group_reduce<LPU, false>(limb_sum8(t2, 2));
       if (u < units) {
-        const int qd = u >> 2, gq = u & 3, eg0 = 8 * sub, cq = gq * 4 + (eg0 >> 5);
-        store_limbs<BITS>(xq + (qd * kCPQ + cq) * 96, 48, eg0 & 31, t0, t1, t2);
+        const int qd = u >> 2, gq = u & 3, eg0 = 8 * sub, cqd = gq * 4 + (eg0 >> 5);
+        store_limbs<BITS>(xq + (qd * kCPQ + cqd) * 96, 48, eg0 & 31, t0, t1, t2);
         if (sub == 0) {
           constexpr int OFF = code_offset<BITS>();
           const i32x4 mv = {-OFF * b0, -OFF * b1, -OFF * b2, act_scale_bits(e)};
@@ -219,6 +217,7 @@ __global__ void __launch_bounds__(1024, 1) i8_m1d_kernel(const I8Args a) {
     convert(p0);
   }
   __syncthreads();
+  AK_M1_STAMP(2);
 
   // A role: group c >> 2, limb c & 3 (limb 3 reads the zero region), chunk 4 * (c >> 2) + h of the quad
   const bool a_on = (c & 3) < 3;
@@ -231,120 +230,198 @@ __global__ void __launch_bounds__(1024, 1) i8_m1d_kernel(const I8Args a) {
     if (lane < 4) yl[bl * 4 + lane] = f2bf(y);
   };
 
-  float acc = 0.f, yrun = 0.f;
-  auto item = [&](const Cursor& x, const Raw<BITS>& bf, uint32_t sraw) {
-    const int qd = x.qd, p = x.p;
-    if (qd == p) acc = 0.f;  // first quad of this stripe
-    i32x4 d = meta[qd * 4 + h];
-    const float sE = __uint_as_float(vv & 1 ? sraw & 0xFFFF0000u : sraw << 16) * __int_as_float(d[3]);
-    i32x4 b0, b1;
-    make_b<BITS>(bf, b0, b1);
-    const uint8_t* src = lds + a_base + qd * a_qmul;
+  // the scale's half of the loaded dword into the high half of an fp32 (v_perm selector per lane), and the source
+  // lanes of a stripe partial's four slots (ds_bpermute byte addresses), both loop-invariant
+  const uint32_t ssel = vv & 1 ? 0x07060C0Cu : 0x05040C0Cu;
+  const int r4 = 4 * (lane & 3);
+  const int sl0 = 4 * r4, sl1 = 4 * (17 + r4), sl2 = 4 * (34 + r4), sl3 = 4 * (51 + r4);
+
+  // compute cursor: block, quad, stripe
+  int cb = b0w, cq = qa, cp = pa;
+  float acc[RB], yrun[RB];
+#pragma unroll
+  for (int r = 0; r < RB; ++r) acc[r] = 0.f, yrun[r] = 0.f;
+  // one item without branches: an[] = the accumulators before a stripe end reset them (used only at a stripe end)
+  auto core = [&](const Raw<BITS> (&bf)[RB], const uint32_t (&sraw)[RB], float (&an)[RB], bool& end, int& eg,
+                  int& ep) {
+    const i32x4 m = meta[cq * 4 + h];
+    const uint8_t* src = lds + a_base + cq * a_qmul;
     const i32x4 a0 = *reinterpret_cast<const i32x4*>(src);
     const i32x4 a1 = *reinterpret_cast<const i32x4*>(src + 48);
-    d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, d, 0, 0, 0);
-    d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, d, 0, 0, 0);
-    acc = fmaf(group_sum_f32(d), sE, acc);
-    if (qd + P < nquad) return;  // more quads in this stripe
-    // stripe partial of row r = lane (lanes 0..3): ((slot 0 + slot 1) + slot 2) + slot 3, slot v in lane 17 v + 4 r
-    const int r4 = 4 * (lane & 3);
-    const float v0 = __shfl(acc, r4), v1 = __shfl(acc, 17 + r4), v2 = __shfl(acc, 34 + r4), v3 = __shfl(acc, 51 + r4);
-    const float pp = ((v0 + v1) + v2) + v3;
+    const int r0 = cq - qa;
+    end = ((r0 < 64 ? ends0 >> r0 : ends1 >> (r0 - 64)) & 1ull) != 0;
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      const float sE = __uint_as_float(__builtin_amdgcn_perm(sraw[r], sraw[r], ssel)) * __int_as_float(m[3]);
+      i32x4 b0, b1;
+      make_b<BITS>(bf[r], b0, b1);
+      i32x4 d = m;
+      d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, d, 0, 0, 0);
+      d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, d, 0, 0, 0);
+      an[r] = fmaf(group_sum_f32(d), sE, acc[r]);
+      acc[r] = end ? 0.f : an[r];
+    }
+    eg = cb;
+    ep = cp;
+    cp = end ? cp + 1 : cp;
+    const bool wrap = cq + 1 == qb;
+    cq = wrap ? qa : cq + 1;
+    cb = wrap ? cb + bstep : cb;
+    cp = wrap ? pa : cp;
+  };
+  // a stripe ended with accumulators v[]: its partial per row (lanes 0..3: ((slot 0 + slot 1) + slot 2) + slot 3,
+  // slot v of row r in lane 17v + 4r), then the blocks' outputs when the task ends
+  auto stripe_end = [&](const float (&v)[RB], int eg, int ep) {
+    float pp[RB];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      const int vi = __float_as_int(v[r]);
+      const float v0 = __int_as_float(__builtin_amdgcn_ds_bpermute(sl0, vi)),
+                  v1 = __int_as_float(__builtin_amdgcn_ds_bpermute(sl1, vi)),
+                  v2 = __int_as_float(__builtin_amdgcn_ds_bpermute(sl2, vi)),
+                  v3 = __int_as_float(__builtin_amdgcn_ds_bpermute(sl3, vi));
+      pp[r] = ((v0 + v1) + v2) + v3;
+    }
     if constexpr (SPLIT == 1) {
-      yrun = p == 0 ? pp : yrun + pp;
-      if (p == P - 1) write_y(x.b, yrun);
+#pragma unroll
+      for (int r = 0; r < RB; ++r) {
+        yrun[r] = ep == 0 ? pp[r] : yrun[r] + pp[r];
+        if (ep == P - 1 && eg * RB + r < nb) write_y(eg * RB + r, yrun[r]);
+      }
     } else {
-      float* slot = part + x.b * P * 4;
-      if (lane < 4) slot[p * 4 + lane] = pp;
-      if (p + SPLIT < P) return;  // more stripes in this task
+#pragma unroll
+      for (int r = 0; r < RB; ++r)
+        if (lane < 4 && eg * RB + r < nb) part[((eg * RB + r) * P + ep) * 4 + lane] = pp[r];
+      if (ep + 1 < pb) return;  // more stripes in this task
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");  // LDS only: no wait for loads in flight
       int last = 0;
-      if (lane == 0) last = atomicAdd(&tickets[x.b], 1) == SPLIT - 1;
+      if (lane == 0) last = atomicAdd(&tickets[eg], 1) == SPLIT - 1;
       last = __shfl(last, 0);
       if (last) {
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-        float y = slot[lane & 3];
-        for (int q = 1; q < P; ++q) y += slot[q * 4 + (lane & 3)];
-        write_y(x.b, y);
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+          if (eg * RB + r >= nb) continue;
+          const float* slot = part + (eg * RB + r) * P * 4;
+          float y = slot[lane & 3];
+          for (int q = 1; q < P; ++q) y += slot[q * 4 + (lane & 3)];
+          write_y(eg * RB + r, y);
+        }
       }
     }
   };
 
-  // full rounds of DEPTH: the compute of an item past the end is skipped (a wave-uniform branch that leaves the
-  // buffers alone), its fetch is not, so the buffer registers stay fixed and the load counters exact
-  Cursor cc;
-  start(cc, wave);
-  for (int i0 = 0; i0 < nitems; i0 += DEPTH) {
+  const int nfull = nitems / DEPTH * DEPTH;
+  for (int i0 = 0; i0 < nfull; i0 += DEPTH) {
+    float sv[DEPTH][RB];
+    bool end[DEPTH];
+    int eg[DEPTH], ep[DEPTH];
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) {
-      if (i0 + d < nitems) item(cc, buf[d], sbuf[d]);
+      core(buf[d], sbuf[d], sv[d], end[d], eg[d], ep[d]);
       fetch_next(buf[d], sbuf[d]);
-      advance(cc);
+    }
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d)
+      if (end[d]) stripe_end(sv[d], eg[d], ep[d]);
+  }
+  // the last, partial group (its later fetches load the cache-resident dummy item)
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d) {
+    if (nfull + d < nitems) {
+      float v[RB];
+      bool e;
+      int g, p;
+      core(buf[d], sbuf[d], v, e, g, p);
+      if (e) stripe_end(v, g, p);
     }
   }
+  AK_M1_STAMP(3);
   __syncthreads();
   for (int i = tid; i < nb * 4; i += 64 * nwv) {
-    const int g = b_lo * 4 + i;
-    const int sg = seg_of(sgs, g);
-    const int orow = g - (sg ? AK_PICK(sg - 1, sgs.end) : 0);
-    if (orow < AK_PICK(sg, sgs.n)) AK_PICK(sg, sgs.y)[orow] = yl[i];
+    const int row = (b_lo * 4) + i;
+    if (row < n) yseg[row] = yl[i];
   }
 }
 
 size_t m1d_x_bytes(int nquad) { return 512 + (size_t)nquad * (kCPQ * 96 + 4 * 16); }
 size_t m1d_block_bytes(int P, int split) { return 8 + (split > 1 ? (size_t)P * 16 + 4 : 0); }  // per 4-row block
 
-template <int BITS, int SPLIT>
+template <int BITS, int SPLIT, int RB>
 void launch_split(const I8Args& a, int grid, int nwv, size_t smem, hipStream_t s) {
-  constexpr int DEPTH = 8;  // items in flight per wave
-  hipLaunchKernelGGL((i8_m1d_kernel<BITS, SPLIT, DEPTH>), dim3(grid), dim3(64 * nwv), smem, s, a);
+  constexpr int DEPTH = RB == 1 ? 4 : 2;  // items in flight per wave (block-items: 4)
+  hipLaunchKernelGGL((i8_m1d_kernel<BITS, SPLIT, DEPTH, RB>), dim3(grid), dim3(64 * nwv), smem, s, a);
 }
 
 template <int BITS>
-int launch_m1d(const I8Args& a, hipStream_t s) {
-  const int n_b4 = a.segs.end[a.segs.nseg - 1] / 4;
+int launch_m1d(I8Args a, hipStream_t s) {
+  const Segs& g = a.segs;
   const size_t x_bytes = m1d_x_bytes(a.nquad);
   const int tiles = kpad(a.k) >> 10;
-  for (int i = 0; i < a.segs.nseg; ++i)  // buffer offsets are 32-bit
-    if ((long long)tiles * a.segs.n[i] * 128 * BITS >= (1ll << 31)) return AK_INVALID;
+  for (int i = 0; i < g.nseg; ++i)  // buffer offsets are 32-bit
+    if ((long long)tiles * g.n[i] * 128 * BITS >= (1ll << 31)) return AK_INVALID;
   if (x_bytes > 150 * 1024) return AK_INVALID;
-  const int grid = n_b4 < num_cus() ? n_b4 : num_cus();
-  const int nbmax = (n_b4 + grid - 1) / grid;
-  // waves per workgroup and waves per block: fewest item rounds of the busiest wave, counting a task's overhead as
-  // about one item; ties go to more waves (latency hiding) and to fewer waves per block (less exchange)
-  int best_split = 1, best_nwv = 16;
+  // workgroups per segment: about the same number of blocks each, at most one workgroup per CU
+  int total = 0;
+  for (int i = 0; i < g.nseg; ++i) total += (g.n[i] + 3) / 4;
+  const int cus = num_cus();
+  int per = (total + cus - 1) / cus, grid = 0;
+  for (;; ++per) {
+    grid = 0;
+    for (int i = 0; i < g.nseg; ++i) grid += ((g.n[i] + 3) / 4 + per - 1) / per;
+    if (grid <= cus || per >= total) break;
+  }
+  for (int i = 0, e = 0; i < kMaxSegs; ++i) {
+    if (i < g.nseg) e += ((g.n[i] + 3) / 4 + per - 1) / per;
+    a.wg_end[i] = e;
+  }
+  int nbmax = 0;
+  for (int i = 0; i < g.nseg; ++i) {
+    const int nbs = (g.n[i] + 3) / 4, gs = (nbs + per - 1) / per;
+    nbmax = (nbs + gs - 1) / gs > nbmax ? (nbs + gs - 1) / gs : nbmax;
+  }
+  // waves per workgroup, waves per block and blocks per item: fewest item rounds for the busiest wave, a task's
+  // overhead counted as about one item and a two-block item as 1.7 items; ties go to more waves (latency hiding),
+  // fewer waves per block (less exchange) and single blocks (finer balance)
+  int best_split = 1, best_nwv = 16, best_rb = 1;
   double best = 1e30;
-  for (int nwv : {16, 12, 8})
-    for (int split : {1, 2, 4, 8}) {
-      if (split > a.P) break;
-      if (x_bytes + (size_t)nbmax * m1d_block_bytes(a.P, split) + 16 > 160 * 1024) continue;
-      const int tasks = nbmax * split;
-      const int per_wave = (tasks + nwv - 1) / nwv;
-      const int items = (a.P + split - 1) / split * ((a.nquad + a.P - 1) / a.P);
-      const double cost = per_wave * (items + 1.0);
-      if (cost < best - 1e-9) best = cost, best_split = split, best_nwv = nwv;
-    }
+  for (int rb : {1, 2})
+    for (int nwv : {16, 8})
+      for (int split : {1, 2, 4, 8}) {
+        if (split > a.P) break;
+        if (x_bytes + (size_t)nbmax * m1d_block_bytes(a.P, split) + 16 > 160 * 1024) continue;
+        int lmax = 0;
+        for (int j = 0; j < split; ++j) {
+          const int l =
+              stripe_begin((j + 1) * a.P / split, a.nquad, a.P) - stripe_begin(j * a.P / split, a.nquad, a.P);
+          lmax = l > lmax ? l : lmax;
+        }
+        const int bstep = nwv / split, ngmax = (nbmax + rb - 1) / rb;
+        const double cost = (double)((ngmax + bstep - 1) / bstep) * (lmax * (rb == 1 ? 1.0 : 1.7) + 1.0);
+        if (cost < best - 1e-9) best = cost, best_split = split, best_nwv = nwv, best_rb = rb;
+      }
   if (best > 1e29) return AK_INVALID;
   const size_t smem = x_bytes + (size_t)nbmax * m1d_block_bytes(a.P, best_split) + 16;
-  switch (best_split) {
-    case 1: launch_split<BITS, 1>(a, grid, best_nwv, smem, s); break;
-    case 2: launch_split<BITS, 2>(a, grid, best_nwv, smem, s); break;
-    case 4: launch_split<BITS, 4>(a, grid, best_nwv, smem, s); break;
-    default: launch_split<BITS, 8>(a, grid, best_nwv, smem, s); break;
+  switch (best_split * 10 + best_rb) {
+    case 11: launch_split<BITS, 1, 1>(a, grid, best_nwv, smem, s); break;
+    case 21: launch_split<BITS, 2, 1>(a, grid, best_nwv, smem, s); break;
+    case 41: launch_split<BITS, 4, 1>(a, grid, best_nwv, smem, s); break;
+    case 81: launch_split<BITS, 8, 1>(a, grid, best_nwv, smem, s); break;
+    case 12: launch_split<BITS, 1, 2>(a, grid, best_nwv, smem, s); break;
+    case 22: launch_split<BITS, 2, 2>(a, grid, best_nwv, smem, s); break;
+    case 42: launch_split<BITS, 4, 2>(a, grid, best_nwv, smem, s); break;
+    default: launch_split<BITS, 8, 2>(a, grid, best_nwv, smem, s); break;
   }
   return (int)hipGetLastError();
 }
 
 }  // namespace
 
-// one token, group 128; the segments' row ranges are re-padded to 4 rows.  Returns AK_INVALID if the shape does not
-// suit the kernel (activations beyond the LDS, a segment beyond 2 GB): the caller falls back.
-int i8_gemv_m1d(int bits, const void* x, const Segs& g0, int k, hipStream_t s) {
-  Segs g = g0;
-  for (int i = 0, e = 0; i < g.nseg; ++i) {
-    e += (g.n[i] + 3) / 4 * 4;
-    g.end[i] = e;
-  }
+// one token; each segment's rows are processed in 4-row blocks (the last one padded).  Returns AK_INVALID if the shape
+// does not suit the kernel (group 64, activations beyond the LDS, a segment beyond 2 GB): the caller falls back to the
+// any-m kernel.
+int i8_gemv_m1(int bits, const void* x, const Segs& g, int k, int group, hipStream_t s) {
+  if (group != kG) return AK_INVALID;
   I8Args a;
   a.segs = g;
   a.x = static_cast<const uint16_t*>(x);
@@ -353,7 +430,6 @@ int i8_gemv_m1d(int bits, const void* x, const Segs& g0, int k, hipStream_t s) {
   a.nquad = kpad(k) / kG / 4;
   a.P = a.nquad < 8 ? a.nquad : 8;
   a.nb = 0;
-  a.iters_max = 1;
   switch (bits) {
     case 4: return launch_m1d<4>(a, s);
     case 3: return launch_m1d<3>(a, s);

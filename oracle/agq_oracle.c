@@ -350,7 +350,8 @@ void ora_gemv_fast_kt_rows(int bits, const uint16_t* x, int m, const uint8_t* wt
       const uint16_t* xr = x + (size_t)j * k;
       float acc[8][4];
       memset(acc, 0, sizeof(acc));
-      for (int qd = 0; qd < nquad; ++qd)
+      for (int qd = 0, p = 0; qd < nquad; ++qd) {
+        while (qd >= (p + 1) * nquad / P) ++p; /* stripe p = quads [p * nquad / P, (p + 1) * nquad / P) */
         for (int s = 0; s < 4; ++s) {
           const int g = 4 * qd + s, t = g * group / 1024, gi = g % SPT;
           int E;
@@ -359,8 +360,9 @@ void ora_gemv_fast_kt_rows(int bits, const uint16_t* x, int m, const uint8_t* wt
           const int T = (int)(D[2] * 256 + D[1]);
           const float gsum = fmaf((float)T, 256.0f, (float)D[0]);
           const float sE = ora_bf2f(st[((size_t)t * n + o) * SPT + gi]) * ldexpf(1.0f, E - 148);
-          acc[qd % P][s] = fmaf(gsum, sE, acc[qd % P][s]);
+          acc[p][s] = fmaf(gsum, sE, acc[p][s]);
         }
+      }
       float yv = 0.f;
       for (int p = 0; p < P; ++p) {
         const float part = ((acc[p][0] + acc[p][1]) + acc[p][2]) + acc[p][3];
