@@ -1,7 +1,8 @@
 """Builds libagens_kernels.so (the C-ABI library of the mixed-bit GEMV path) in-tree with hipcc for gfx950.
 
 Usage: python agens-engine_amd/build.py [--jobs N]
-Objects go to agens-engine_amd/_build/, the library to agens-engine_amd/libagens_kernels.so.
+Objects go to agens-engine_amd/_build/, the library to agens-engine_amd/libagens_kernels.so; also builds the benchmark
+helper libagens_bench.so, the C++ host side libagens_linear.so and its test program tests/host/test_linear.
 """
 import argparse
 import concurrent.futures
@@ -16,6 +17,8 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libagens_kernels.so")
 BENCH_LIB = os.path.join(HERE, "libagens_bench.so")
+HOST = os.path.join(HERE, "host")
+HOST_LIB = os.path.join(HERE, "libagens_linear.so")
 SOURCES = ["ak_runtime.hip", "wq_layout.hip", "wq_exact.hip", "wq_i8.hip", "wq_i8m1d.hip", "wq_api.hip"]
 
 
@@ -67,8 +70,25 @@ def build(jobs=None, verbose=True):
     if r.returncode != 0:
         raise RuntimeError("link failed (bench support):\n" + r.stdout + r.stderr)
     os.replace(tmp, BENCH_LIB)
+    # the C++ host side (agens_linear: uploads, linear, linear_shared) and its GPU test program
+    gxx = shutil.which("g++") or "g++"
+    hflags = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-I" + os.path.join(ROOT, "include"), "-I" + HOST]
+    cmd = [gxx] + hflags + ["-shared", "-o", HOST_LIB + ".tmp", os.path.join(HOST, "agens_linear.cpp"),
+                            "-L" + HERE, "-lagens_kernels", "-Wl,-rpath,$ORIGIN", "-Wl,--no-undefined"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("host library build failed:\n" + r.stdout + r.stderr)
+    os.replace(HOST_LIB + ".tmp", HOST_LIB)
+    test_src = os.path.join(ROOT, "tests", "host", "test_linear.cpp")
+    test_bin = os.path.join(ROOT, "tests", "host", "test_linear")
+    cmd = [gxx] + hflags + ["-o", test_bin + ".tmp", test_src, "-L" + HERE, "-lagens_linear", "-lagens_kernels",
+                            "-Wl,-rpath," + HERE]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("host test build failed:\n" + r.stdout + r.stderr)
+    os.replace(test_bin + ".tmp", test_bin)
     if verbose:
-        print(f"built {LIB} and {BENCH_LIB}")
+        print(f"built {LIB}, {BENCH_LIB}, {HOST_LIB} and {test_bin}")
     return LIB
 
 

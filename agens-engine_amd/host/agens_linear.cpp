@@ -1,0 +1,140 @@
+// Host side of the quantized-linear path (see agens_linear.h).
+#include "agens_linear.h"
+
+#include "agens_kernels.h"
+
+namespace agens {
+
+void check(int code, const char* what) {
+  if (code == 0) return;
+  const char* msg = ak_error_string(code);
+  throw Error(std::string(what) + ": error " + std::to_string(code) + " (" + (msg ? msg : "?") + ")");
+}
+
+DeviceBuffer::DeviceBuffer(size_t bytes) : bytes_(bytes) {
+  check(ak_malloc(&ptr_, bytes ? bytes : 1), "malloc");
+}
+DeviceBuffer::DeviceBuffer(DeviceBuffer&& o) noexcept : ptr_(o.ptr_), bytes_(o.bytes_) { o.ptr_ = nullptr; }
+DeviceBuffer& DeviceBuffer::operator=(DeviceBuffer&& o) noexcept {
+  if (this != &o) {
+    if (ptr_) ak_free(ptr_);
+    ptr_ = o.ptr_, bytes_ = o.bytes_, o.ptr_ = nullptr;
+  }
+  return *this;
+}
+DeviceBuffer::~DeviceBuffer() {
+  if (ptr_) ak_free(ptr_);
+}
+void* DeviceBuffer::leak() {
+  void* p = ptr_;
+  ptr_ = nullptr;
+  return p;
+}
+
+DeviceBuffer device_alloc(size_t bytes) { return DeviceBuffer(bytes); }
+
+DeviceBuffer upload(const void* host, size_t bytes) {
+  DeviceBuffer b(bytes);
+  check(ak_memcpy_h2d(b.ptr(), host, bytes), "memcpy_h2d");
+  return b;
+}
+
+namespace {
+
+void check_sizes(const char* what, const std::vector<uint8_t>& packed, const std::vector<uint8_t>& scales, int n,
+                 int k, int group) {
+  if (n < 1 || k < 1 || group < 1 || packed.size() != (size_t)n * k / 2 ||
+      scales.size() != (size_t)n * (k / group) * 2)
+    throw Error(std::string(what) + ": " + std::to_string(packed.size()) + " / " + std::to_string(scales.size()) +
+                " bytes for [" + std::to_string(n) + ", " + std::to_string(k) + "] group " + std::to_string(group));
+}
+
+// repack through the C ABI; returns its code (1: a value outside `bits` bits, or bad arguments)
+int repack(int bits, const std::vector<uint8_t>& packed, const std::vector<uint8_t>& scales, int n, int k, int group,
+           KtPair& out) {
+  DeviceBuffer p = upload(packed.data(), packed.size()), s = upload(scales.data(), scales.size());
+  out.first = device_alloc(ak_wq_kt_weight_bytes(bits, n, k));
+  out.second = device_alloc(ak_w4_kt_scale_bytes(n, k, group));
+  const int e = ak_wq_repack_kt(bits, static_cast<const int32_t*>(p.ptr()), s.ptr(), out.first.ptr(),
+                                out.second.ptr(), n, k, group, nullptr);
+  // the staging buffers are freed when p and s go out of scope: wait for the repack to have read them
+  const int e2 = ak_synchronize();
+  return e ? e : e2;
+}
+
+}  // namespace
+
+KtPair w4_upload_kt(const std::vector<uint8_t>& packed, const std::vector<uint8_t>& scales, int n, int k, int group) {
+  check_sizes("w4_upload_kt", packed, scales, n, k, group);
+  KtPair out;
+  check(repack(4, packed, scales, n, k, group, out), "w4_repack_kt");
+  return out;
+}
+
+std::optional<KtPair> w3_upload_kt(const std::vector<uint8_t>& packed, const std::vector<uint8_t>& scales, int n,
+                                   int k, int group) {
+  check_sizes("w3_upload_kt", packed, scales, n, k, group);
+  KtPair out;
+  const int e = repack(3, packed, scales, n, k, group, out);
+  if (e == 1) return std::nullopt;  // a 4-bit value
+  check(e, "w3_repack_kt");
+  return out;
+}
+
+KtPair wq_upload_kt(int bits, const std::vector<uint8_t>& packed, const std::vector<uint8_t>& scales, int n, int k,
+                    int group) {
+  if (bits == 4) return w4_upload_kt(packed, scales, n, k, group);
+  check_sizes("wq_upload_kt", packed, scales, n, k, group);
+  KtPair out;
+  const int e = repack(bits, packed, scales, n, k, group, out);
+  if (e == 1)
+    throw Error("wq_upload_kt: [" + std::to_string(n) + ", " + std::to_string(k) + "] has values outside " +
+                std::to_string(bits) + " bits");
+  check(e, "wq_repack_kt");
+  return out;
+}
+
+int linear(const QuantLinear& t, const void* x, void* y, int m, int n, int k, int bf16w, void* stream) {
+  if (t.n != n || t.k != k || m < 1 || m > 128 || t.np < 1 || t.np > 2) return 1;
+  for (int j = 0; j < t.np; ++j) {
+    const QuantPart& q = t.p[j];
+    void* yp = static_cast<uint16_t*>(y) + q.r0;
+    const void* wt = q.wt;
+    const void* st = q.st;
+    const int e = ak_wq_gemv_kt_multi(q.bits, x, m, 1, &wt, &st, &yp, &q.n, &n, k, q.group, bf16w, stream);
+    if (e) return e;
+  }
+  return 0;
+}
+
+int linear_shared(const void* x, int nl, const QuantLinear* const* lins, void* const* ys, const int* ns, int m, int k,
+                  int bf16w, void* stream) {
+  bool ok = nl >= 1 && nl <= 4 && m == 1;
+  for (int j = 0; j < nl && ok; ++j) ok = lins[j] && lins[j]->np == 1 && lins[j]->n == ns[j] && lins[j]->k == k;
+  if (ok) {  // one launch per (bits, group) class
+    bool done[4] = {false, false, false, false};
+    for (int j = 0; j < nl; ++j) {
+      if (done[j]) continue;
+      const QuantPart& pj = lins[j]->p[0];
+      const void *wt[4], *st[4];
+      void* y[4];
+      int nn[4], c = 0;
+      for (int i = j; i < nl; ++i) {
+        const QuantPart& pi = lins[i]->p[0];
+        if (done[i] || pi.bits != pj.bits || pi.group != pj.group) continue;
+        wt[c] = pi.wt, st[c] = pi.st, y[c] = ys[i], nn[c] = ns[i], ++c, done[i] = true;
+      }
+      const int e = ak_wq_gemv_kt_multi(pj.bits, x, m, c, wt, st, y, nn, nullptr, k, pj.group, bf16w, stream);
+      if (e) return e;
+    }
+    return 0;
+  }
+  for (int j = 0; j < nl; ++j) {
+    if (!lins[j]) return 1;
+    const int e = linear(*lins[j], x, ys[j], m, ns[j], k, bf16w, stream);
+    if (e) return e;
+  }
+  return 0;
+}
+
+}  // namespace agens

@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the mixed-bit quantized GEMV path on one MI355X.
 
-Headline (BASELINE.json metric): effective HBM GB/s (and % of the 8 TB/s peak) and microseconds per 64-layer
+Headline metric: effective HBM GB/s (and % of the 8 TB/s peak) and microseconds per 64-layer
 32B-shaped decode GEMV sweep at M = 1: per layer QKV (5120 -> 7168 as q/k/v segments of one launch), O (5120 -> 5120),
 gate_up (5120 -> 55296) and down (27648 -> 5120), each layer's bit width drawn from a fixed seed (W2 p=.3, W3 p=.5,
 W4 p=.2), group 128, plus the W4 LM head (5120 -> 152064).  One "step" = one sweep (257 GEMV launches), replayed as
@@ -221,7 +221,7 @@ def cpu_baseline(ctx, m, cpu, budget_s=20.0):
 
 def run_sweep(args, K, B):
     ctx = Ctx(K, B)
-    cpu_layers = 0 if args.no_cpu else 2
+    cpu_layers = 0 if args.no_cpu else 24  # containers kept on the host for the CPU baseline (about 20 s of it)
     t0 = time.time()
     plan, meta, cpu = build_sweep(ctx, args.m, cpu_layers)
     print(f"# sweep generated in {time.time() - t0:.1f} s ({len(plan)} launches)", file=sys.stderr, flush=True)
@@ -233,9 +233,10 @@ def run_sweep(args, K, B):
     # per-launch durations (events around every launch) -> the dominant kernel
     each = (ctypes.c_float * len(plan))()
     ctx.check(B.agb_time_each(arr, len(plan), 3, each), "time each")
+    # the dominant kernel: the launch class (linear, bit width; one kernel instance per shape) with the most time
     by_kernel = {}
     for L, (name, b), t in zip(plan, meta, each):
-        key = f"i8_gemv_kernel<{b},128,{(args.m + 3) // 4}>"
+        key = f"{name}_w{b}"
         d = by_kernel.setdefault(key, {"ms": 0.0, "bytes": 0, "launches": 0})
         d["ms"] += t
         d["bytes"] += algo_bytes(L)
@@ -255,11 +256,11 @@ def run_sweep(args, K, B):
     cpu_res = cpu_baseline(ctx, args.m, cpu) if cpu else None
     bits_mix = {f"w{b}": sum(1 for (_, bb) in meta[:-1] if bb == b) // 4 for b in (2, 3, 4)}
     traffic = None
-    tf = os.path.join(ROOT, "profiles", "traffic_sweep_m1.json")
+    tf = os.path.join(ROOT, "profiles", "traffic.json")  # HBM bytes per launch from rocprofv3 FETCH_SIZE / WRITE_SIZE
     if args.m == 1 and os.path.exists(tf):
         try:
-            traffic = json.load(open(tf)).get(dom_name)
-        except Exception:
+            traffic = json.load(open(tf)).get(dom_name, {}).get("bytes_per_launch")
+        except (OSError, ValueError):
             traffic = None
     out = {
         "metric": "effective HBM GB/s (% of peak) + us per 64-layer 32B decode GEMV sweep, M=1",
@@ -273,7 +274,7 @@ def run_sweep(args, K, B):
                                "+ W4 LM head 5120->152064",
                    "m": args.m, "layers_by_bits": bits_mix, "launches": len(plan),
                    "bytes_per_sweep": total_bytes, "graph": not args.eager, "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "kernel": dom_name, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+        "roofline": {"bound": "hbm", "kernel": f"i8_m1d_kernel ({dom_name})", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "launches": dom["launches"], "avg_us": round(dom["ms"] * 1e3 / dom["launches"], 2),
                      "bytes_per_launch": dom["bytes"] // dom["launches"]},
@@ -325,10 +326,12 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true")
     ap.add_argument("--exact", action="store_true", help="the reference's exact fp32 numerics instead")
+    ap.add_argument("--calib", action="store_true",
+                    help="first copy 256 MiB with a plain copy kernel (the known-size reference for HBM counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (the GEMV shards by output rows with no "
-              "communication, or by k with one all-reduce; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        print("bench.py measures one GPU: this build has no multi-GPU path (the GEMV would shard by output rows with "
+              "no communication, or by k with one all-reduce of the outputs). Run with --gpus 1.", file=sys.stderr)
         return 2
     K, B = load_libs()
     for fn in ("ak_w4_set_lean", "ak_w4_set_mma"):
@@ -338,6 +341,10 @@ def main():
     name = ctypes.create_string_buffer(128)
     K.ak_device_name(0, name, 128)
     print(f"# device {name.value.decode()}", file=sys.stderr, flush=True)
+    if args.calib:
+        B.agb_copy.argtypes, B.agb_copy.restype = [ctypes.c_size_t, ctypes.c_int], ctypes.c_int
+        if B.agb_copy(256 << 20, 2):
+            raise RuntimeError("calibration copy failed")
     if args.config == "sweep":
         print(json.dumps(run_sweep(args, K, B)), flush=True)
     else:

@@ -32,7 +32,7 @@ def test_sizes_match_layout(K):
         assert K.ak_w3_kt_weight_bytes(n, k) == O.ora_kt_weight_bytes(3, n, k)
         for g in (64, 128):
             assert K.ak_w4_kt_scale_bytes(n, k, g) == O.ora_kt_scale_bytes(n, k, g)
-    # BASELINE config 1 / 2 sizes: W3 55296 x 5120 and W2 5120 x 27648
+    # the fused gate+up W3 55296 x 5120 and the down W2 5120 x 27648 shapes (w4_gemv.cu:560-563, 821-822)
     assert K.ak_wq_kt_weight_bytes(3, 55296, 5120) == 106168320
     assert K.ak_w4_kt_scale_bytes(55296, 5120, 128) == 4423680
     assert K.ak_wq_kt_weight_bytes(2, 5120, 27648) == 35389440
