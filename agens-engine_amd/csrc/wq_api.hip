@@ -15,7 +15,7 @@ namespace agq {
 int exact_gemv(int bits, const void* x, int m, const Segs& g, int k, int group, int bf16w, hipStream_t s);
 int exact_ct_gemv(const void* x, const int32_t* packed, const void* scales, void* y, int n, int k, hipStream_t s);
 int i8_gemv(int bits, const void* x, int m, const Segs& g, int k, int group, hipStream_t s);
-int i8_gemv_m1(int bits, const void* x, const Segs& g, int k, int group, hipStream_t s);
+int i8_gemv_m1(int bits, const void* x, int m, const Segs& g, int k, int group, hipStream_t s);
 
 namespace {
 
@@ -52,12 +52,23 @@ Segs make_segs(int nseg, const void* const* wt, const void* const* st, void* con
   return g;
 }
 
-// one launch of the default path, m <= 16 (one token: the decode kernel, when its activations fit the LDS)
+// the default path for m <= 16 tokens: the line-load kernel (wq_i8m1d.hip) for up to 8 tokens at a time when the
+// tokens' activations fit its LDS, otherwise the any-m kernel (wq_i8.hip)
 int run_i8(int bits, const void* x, int m, const Segs& g, int k, int group, hipStream_t s) {
-  if (m == 1) {
-    const int e = i8_gemv_m1(bits, x, g, k, group, s);
-    if (e != AK_INVALID) return e;
+  const int mt = m <= 8 ? m : (m + 1) / 2;
+  bool ok = true;
+  for (int m0 = 0; m0 < m && ok; m0 += mt) {
+    const int mm = m - m0 < mt ? m - m0 : mt;
+    Segs gg = g;
+    for (int i = 0; i < g.nseg; ++i) gg.y[i] = g.y[i] + (size_t)m0 * g.ldy[i];
+    const int e = i8_gemv_m1(bits, static_cast<const uint16_t*>(x) + (size_t)m0 * k, mm, gg, k, group, s);
+    if (e == AK_INVALID && m0 == 0) {
+      ok = false;
+    } else if (e) {
+      return e;
+    }
   }
+  if (ok) return 0;
   return i8_gemv(bits, x, m, g, k, group, s);
 }
 

@@ -64,12 +64,12 @@ __device__ __forceinline__ T pick4(int i, T v0, T v1, T v2, T v3) {
 #define AK_PICK(i, arr) pick4((i), (arr)[0], (arr)[1], (arr)[2], (arr)[3])
 static_assert(kMaxSegs == 4, "segment selects cover four segments");
 
-template <int BITS, int SPLIT, int DEPTH, int RB>
+template <int BITS, int SPLIT, int DEPTH, int RB, int MT>
 __global__ void __launch_bounds__(1024, 1) i8_m1d_kernel(const I8Args a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   constexpr int LPU = kG / 8, UPW = 64 / LPU, XB = 4;
   constexpr int REC = Rec<BITS>::bytes, CHB = Rec<BITS>::chunk;
-  const int P = a.P, nquad = a.nquad, k = a.k;
+  const int P = a.P, nquad = a.nquad, k = a.k, mm = a.m;  // mm <= MT tokens (the others are zero, not written)
   const int nwv = blockDim.x >> 6;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -86,14 +86,18 @@ __global__ void __launch_bounds__(1024, 1) i8_m1d_kernel(const I8Args a) {
   const int b_lo = (int)((long long)w * n_b4 / gs);
   const int nb = (int)((long long)(w + 1) * n_b4 / gs) - b_lo;
   uint16_t* const yseg = AK_PICK(sg, sgs.y);
+  const int ldy = AK_PICK(sg, sgs.ldy);
 
-  // LDS: zeros [512 B] | limbs [nquad][16][2][3][16 B] | meta [nquad][4] int4 | outputs [nb][4] bf16 |
-  //      partials [nb][P][4] | tickets [nb]
+  // LDS: zeros [512 B] | limbs [MT][nquad][half 2][chunk 16][limb 3][16 B] | meta [MT][nquad][4] int4 |
+  //      outputs [MT][nb][4] bf16 | partials [nb][P][MT][4] | tickets [nb]
+  // (48-byte chunk stride: the 12 active lanes of each 16-lane pass of an A read hit 12 distinct 16-byte bank slots of
+  // the 256-byte bank row, and the 4 zero-operand lanes read zeros placed in the 4 remaining slots)
+  const int tstride = nquad * kCPQ * 96;  // limbs of one token
   uint8_t* xq = lds + 512;
-  i32x4* meta = reinterpret_cast<i32x4*>(xq + nquad * kCPQ * 96);
-  uint16_t* yl = reinterpret_cast<uint16_t*>(meta + nquad * 4);
-  float* part = reinterpret_cast<float*>(yl + ((nb * 4 + 3) & ~3));
-  int* tickets = reinterpret_cast<int*>(part + (SPLIT > 1 ? nb * P * 4 : 0));
+  i32x4* meta = reinterpret_cast<i32x4*>(xq + MT * tstride);
+  uint16_t* yl = reinterpret_cast<uint16_t*>(meta + MT * nquad * 4);
+  float* part = reinterpret_cast<float*>(yl + ((MT * nb * 4 + 3) & ~3));
+  int* tickets = reinterpret_cast<int*>(part + (SPLIT > 1 ? nb * P * MT * 4 : 0));
 
   if (SPLIT > 1)
     for (int i = tid; i < nb; i += 64 * nwv) tickets[i] = 0;
@@ -101,7 +105,8 @@ __global__ void __launch_bounds__(1024, 1) i8_m1d_kernel(const I8Args a) {
 
   // ---- activations, step 1: this lane's bf16 inputs, requested and waited for before any weight request (behind
   // the weight requests of the whole GPU, x would arrive microseconds late)
-  const int sub = lane % LPU, units = nquad * 4, ustride = nwv * UPW;
+  const int gpt = nquad * 4;  // groups per token
+  const int sub = lane % LPU, units = gpt * MT, ustride = nwv * UPW;
   const int u0 = wave * UPW + lane / LPU;
   const int npass = (units + ustride - 1) / ustride;
   uint4 xv[XB];
@@ -109,11 +114,11 @@ __global__ void __launch_bounds__(1024, 1) i8_m1d_kernel(const I8Args a) {
 #pragma unroll
     for (int b = 0; b < XB; ++b) {
       // lanes past the end load x[0] (zero-selected); passes past npass load nothing (a wave-uniform branch)
-      const int u = u0 + (pass0 + b) * ustride, kk = u * kG + 8 * sub;
-      const bool ok = u < units && kk < k;
+      const int u = u0 + (pass0 + b) * ustride, t = MT == 1 ? 0 : u / gpt, kk = (u - t * gpt) * kG + 8 * sub;
+      const bool ok = u < units && t < mm && kk < k;
       xv[b] = make_uint4(0u, 0u, 0u, 0u);
       if (pass0 + b < npass) {
-        const uint4 v = *reinterpret_cast<const uint4*>(a.x + (ok ? kk : 0));
+        const uint4 v = *reinterpret_cast<const uint4*>(a.x + (ok ? (size_t)t * k + kk : 0));
         xv[b] = ok ? v : make_uint4(0u, 0u, 0u, 0u);
       }
     }
@@ -201,8 +206,9 @@ __global__ void __launch_bounds__(1024, 1) i8_m1d_kernel(const I8Args a) {
       const int b1 = dpp_group_reduce<LPU, false>(limb_sum8(t1, 1));
       const int b2 = dpp_group_reduce<LPU, false>(limb_sum8(t2, 2));
       if (u < units) {
-        const int qd = u >> 2, gq = u & 3, eg0 = 8 * sub, cqd = gq * 4 + (eg0 >> 5);
-        store_limbs<BITS>(xq + (qd * kCPQ + cqd) * 96, 48, eg0 & 31, t0, t1, t2);
+        const int t = MT == 1 ? 0 : u / gpt, ut = u - t * gpt;
+        const int qd = ut >> 2, gq = ut & 3, eg0 = 8 * sub, cqd = gq * 4 + (eg0 >> 5);
+        store_limbs<BITS>(xq + t * tstride + qd * kCPQ * 96 + cqd * 48, kCPQ * 48, eg0 & 31, t0, t1, t2);
         if (sub == 0) {
           constexpr int OFF = code_offset<BITS>();
           const i32x4 mv = {-OFF * b0, -OFF * b1, -OFF * b2, act_scale_bits(e)};
@@ -219,15 +225,16 @@ __global__ void __launch_bounds__(1024, 1) i8_m1d_kernel(const I8Args a) {
   __syncthreads();
   AK_M1_STAMP(2);
 
-  // A role: group c >> 2, limb c & 3 (limb 3 reads the zero region), chunk 4 * (c >> 2) + h of the quad
+  // A role: group c >> 2, limb c & 3 (limb 3 reads zeros), chunk 4 * (c >> 2) + h of the quad; half 1 is kCPQ * 48
+  // bytes further
   const bool a_on = (c & 3) < 3;
-  const int a_base = a_on ? 512 + (4 * (c >> 2) + h) * 96 + 16 * (c & 3) : 0;
-  const int a_qmul = a_on ? kCPQ * 96 : 0;
+  const int a_base = a_on ? 512 + (4 * (c >> 2) + h) * 48 + 16 * (c & 3) : ((c >> 2) * 64 + 48 + h * 48) & 255;
+  const int a_qmul = a_on ? kCPQ * 96 : 0, a_tmul = a_on ? tstride : 0;
 
   // outputs are staged in LDS and written after the loop: a global store among the streaming loads would make the
   // compiler drain every load in flight
-  auto write_y = [&](int bl, float y) {  // lanes 0..3: row `lane` of local block bl
-    if (lane < 4) yl[bl * 4 + lane] = f2bf(y);
+  auto write_y = [&](int bl, int t, float y) {  // lanes 0..3: row `lane` of local block bl, token t
+    if (lane < 4) yl[(t * nb + bl) * 4 + lane] = f2bf(y);
   };
 
   // the scale's half of the loaded dword into the high half of an fp32 (v_perm selector per lane), and the source
@@ -238,28 +245,38 @@ __global__ void __launch_bounds__(1024, 1) i8_m1d_kernel(const I8Args a) {
 
   // compute cursor: block, quad, stripe
   int cb = b0w, cq = qa, cp = pa;
-  float acc[RB], yrun[RB];
+  float acc[RB][MT], yrun[RB][MT];
 #pragma unroll
-  for (int r = 0; r < RB; ++r) acc[r] = 0.f, yrun[r] = 0.f;
-  // one item without branches: an[] = the accumulators before a stripe end reset them (used only at a stripe end)
-  auto core = [&](const Raw<BITS> (&bf)[RB], const uint32_t (&sraw)[RB], float (&an)[RB], bool& end, int& eg,
+  for (int r = 0; r < RB; ++r)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[r][t] = 0.f, yrun[r][t] = 0.f;
+  // one item without branches: an[][] = the accumulators before a stripe end reset them (used only at a stripe end)
+  auto core = [&](const Raw<BITS> (&bf)[RB], const uint32_t (&sraw)[RB], float (&an)[RB][MT], bool& end, int& eg,
                   int& ep) {
-    const i32x4 m = meta[cq * 4 + h];
-    const uint8_t* src = lds + a_base + cq * a_qmul;
-    const i32x4 a0 = *reinterpret_cast<const i32x4*>(src);
-    const i32x4 a1 = *reinterpret_cast<const i32x4*>(src + 48);
     const int r0 = cq - qa;
     end = ((r0 < 64 ? ends0 >> r0 : ends1 >> (r0 - 64)) & 1ull) != 0;
+    i32x4 b0[RB], b1[RB];
+    float sc[RB];
 #pragma unroll
     for (int r = 0; r < RB; ++r) {
-      const float sE = __uint_as_float(__builtin_amdgcn_perm(sraw[r], sraw[r], ssel)) * __int_as_float(m[3]);
-      i32x4 b0, b1;
-      make_b<BITS>(bf[r], b0, b1);
-      i32x4 d = m;
-      d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, d, 0, 0, 0);
-      d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, d, 0, 0, 0);
-      an[r] = fmaf(group_sum_f32(d), sE, acc[r]);
-      acc[r] = end ? 0.f : an[r];
+      sc[r] = __uint_as_float(__builtin_amdgcn_perm(sraw[r], sraw[r], ssel));
+      make_b<BITS>(bf[r], b0[r], b1[r]);
+    }
+    // token by token: the activation operand and meta of one token are live at a time
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      const i32x4 mt = meta[(t * nquad + cq) * 4 + h];
+      const uint8_t* src = lds + a_base + t * a_tmul + cq * a_qmul;
+      const i32x4 a0 = *reinterpret_cast<const i32x4*>(src);
+      const i32x4 a1 = *reinterpret_cast<const i32x4*>(src + (a_on ? kCPQ * 48 : 0));
+#pragma unroll
+      for (int r = 0; r < RB; ++r) {
+        i32x4 d = mt;
+        d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0[r], d, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1[r], d, 0, 0, 0);
+        an[r][t] = fmaf(group_sum_f32(d), sc[r] * __int_as_float(mt[3]), acc[r][t]);
+        acc[r][t] = end ? 0.f : an[r][t];
+      }
     }
     eg = cb;
     ep = cp;
@@ -269,29 +286,35 @@ __global__ void __launch_bounds__(1024, 1) i8_m1d_kernel(const I8Args a) {
     cb = wrap ? cb + bstep : cb;
     cp = wrap ? pa : cp;
   };
-  // a stripe ended with accumulators v[]: its partial per row (lanes 0..3: ((slot 0 + slot 1) + slot 2) + slot 3,
+  // a stripe ended with accumulators v[][]: its partial per row (lanes 0..3: ((slot 0 + slot 1) + slot 2) + slot 3,
   // slot v of row r in lane 17v + 4r), then the blocks' outputs when the task ends
-  auto stripe_end = [&](const float (&v)[RB], int eg, int ep) {
-    float pp[RB];
+  auto stripe_end = [&](const float (&v)[RB][MT], int eg, int ep) {
+    float pp[RB][MT];
 #pragma unroll
-    for (int r = 0; r < RB; ++r) {
-      const int vi = __float_as_int(v[r]);
-      const float v0 = __int_as_float(__builtin_amdgcn_ds_bpermute(sl0, vi)),
-                  v1 = __int_as_float(__builtin_amdgcn_ds_bpermute(sl1, vi)),
-                  v2 = __int_as_float(__builtin_amdgcn_ds_bpermute(sl2, vi)),
-                  v3 = __int_as_float(__builtin_amdgcn_ds_bpermute(sl3, vi));
-      pp[r] = ((v0 + v1) + v2) + v3;
-    }
+    for (int r = 0; r < RB; ++r)
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        const int vi = __float_as_int(v[r][t]);
+        const float v0 = __int_as_float(__builtin_amdgcn_ds_bpermute(sl0, vi)),
+                    v1 = __int_as_float(__builtin_amdgcn_ds_bpermute(sl1, vi)),
+                    v2 = __int_as_float(__builtin_amdgcn_ds_bpermute(sl2, vi)),
+                    v3 = __int_as_float(__builtin_amdgcn_ds_bpermute(sl3, vi));
+        pp[r][t] = ((v0 + v1) + v2) + v3;
+      }
     if constexpr (SPLIT == 1) {
 #pragma unroll
-      for (int r = 0; r < RB; ++r) {
-        yrun[r] = ep == 0 ? pp[r] : yrun[r] + pp[r];
-        if (ep == P - 1 && eg * RB + r < nb) write_y(eg * RB + r, yrun[r]);
-      }
+      for (int r = 0; r < RB; ++r)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          yrun[r][t] = ep == 0 ? pp[r][t] : yrun[r][t] + pp[r][t];
+          if (ep == P - 1 && eg * RB + r < nb) write_y(eg * RB + r, t, yrun[r][t]);
+        }
     } else {
 #pragma unroll
       for (int r = 0; r < RB; ++r)
-        if (lane < 4 && eg * RB + r < nb) part[((eg * RB + r) * P + ep) * 4 + lane] = pp[r];
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+          if (lane < 4 && eg * RB + r < nb) part[(((eg * RB + r) * P + ep) * MT + t) * 4 + lane] = pp[r][t];
       if (ep + 1 < pb) return;  // more stripes in this task
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");  // LDS only: no wait for loads in flight
       int last = 0;
@@ -302,10 +325,13 @@ __global__ void __launch_bounds__(1024, 1) i8_m1d_kernel(const I8Args a) {
 #pragma unroll
         for (int r = 0; r < RB; ++r) {
           if (eg * RB + r >= nb) continue;
-          const float* slot = part + (eg * RB + r) * P * 4;
-          float y = slot[lane & 3];
-          for (int q = 1; q < P; ++q) y += slot[q * 4 + (lane & 3)];
-          write_y(eg * RB + r, y);
+          const float* slot = part + (eg * RB + r) * P * MT * 4;
+#pragma unroll
+          for (int t = 0; t < MT; ++t) {
+            float y = slot[t * 4 + (lane & 3)];
+            for (int q = 1; q < P; ++q) y += slot[(q * MT + t) * 4 + (lane & 3)];
+            write_y(eg * RB + r, t, y);
+          }
         }
       }
     }
@@ -313,7 +339,7 @@ __global__ void __launch_bounds__(1024, 1) i8_m1d_kernel(const I8Args a) {
 
   const int nfull = nitems / DEPTH * DEPTH;
   for (int i0 = 0; i0 < nfull; i0 += DEPTH) {
-    float sv[DEPTH][RB];
+    float sv[DEPTH][RB][MT];
     bool end[DEPTH];
     int eg[DEPTH], ep[DEPTH];
 #pragma unroll
@@ -329,7 +355,7 @@ __global__ void __launch_bounds__(1024, 1) i8_m1d_kernel(const I8Args a) {
 #pragma unroll
   for (int d = 0; d < DEPTH; ++d) {
     if (nfull + d < nitems) {
-      float v[RB];
+      float v[RB][MT];
       bool e;
       int g, p;
       core(buf[d], sbuf[d], v, e, g, p);
@@ -338,25 +364,27 @@ __global__ void __launch_bounds__(1024, 1) i8_m1d_kernel(const I8Args a) {
   }
   AK_M1_STAMP(3);
   __syncthreads();
-  for (int i = tid; i < nb * 4; i += 64 * nwv) {
-    const int row = (b_lo * 4) + i;
-    if (row < n) yseg[row] = yl[i];
+  for (int i = tid; i < MT * nb * 4; i += 64 * nwv) {
+    const int t = MT == 1 ? 0 : i / (nb * 4), row = b_lo * 4 + i - t * nb * 4;
+    if (t < mm && row < n) yseg[(size_t)t * ldy + row] = yl[i];
   }
 }
 
-size_t m1d_x_bytes(int nquad) { return 512 + (size_t)nquad * (kCPQ * 96 + 4 * 16); }
-size_t m1d_block_bytes(int P, int split) { return 8 + (split > 1 ? (size_t)P * 16 + 4 : 0); }  // per 4-row block
-
-template <int BITS, int SPLIT, int RB>
-void launch_split(const I8Args& a, int grid, int nwv, size_t smem, hipStream_t s) {
-  constexpr int DEPTH = RB == 1 ? 4 : 2;  // items in flight per wave (block-items: 4)
-  hipLaunchKernelGGL((i8_m1d_kernel<BITS, SPLIT, DEPTH, RB>), dim3(grid), dim3(64 * nwv), smem, s, a);
+size_t m1d_x_bytes(int nquad, int mt) { return 512 + (size_t)mt * nquad * (kCPQ * 96 + 4 * 16); }
+size_t m1d_block_bytes(int P, int split, int mt) {  // per 4-row block: outputs, partials, ticket
+  return (size_t)mt * 8 + (split > 1 ? (size_t)P * 16 * mt + 4 : 0);
 }
 
-template <int BITS>
+template <int BITS, int SPLIT, int RB, int MT>
+void launch_split(const I8Args& a, int grid, int nwv, size_t smem, hipStream_t s) {
+  constexpr int DEPTH = RB * MT <= 2 ? 4 / RB : 2;  // items in flight per wave
+  hipLaunchKernelGGL((i8_m1d_kernel<BITS, SPLIT, DEPTH, RB, MT>), dim3(grid), dim3(64 * nwv), smem, s, a);
+}
+
+template <int BITS, int MT>
 int launch_m1d(I8Args a, hipStream_t s) {
   const Segs& g = a.segs;
-  const size_t x_bytes = m1d_x_bytes(a.nquad);
+  const size_t x_bytes = m1d_x_bytes(a.nquad, MT);
   const int tiles = kpad(a.k) >> 10;
   for (int i = 0; i < g.nseg; ++i)  // buffer offsets are 32-bit
     if ((long long)tiles * g.n[i] * 128 * BITS >= (1ll << 31)) return AK_INVALID;
@@ -386,10 +414,11 @@ int launch_m1d(I8Args a, hipStream_t s) {
   int best_split = 1, best_nwv = 16, best_rb = 1;
   double best = 1e30;
   for (int rb : {1, 2})
-    for (int nwv : {16, 8})
+    for (int nwv : {16, 8}) {
+      if (MT > 1 && rb > 1) continue;
       for (int split : {1, 2, 4, 8}) {
         if (split > a.P) break;
-        if (x_bytes + (size_t)nbmax * m1d_block_bytes(a.P, split) + 16 > 160 * 1024) continue;
+        if (x_bytes + (size_t)nbmax * m1d_block_bytes(a.P, split, MT) + 16 > 160 * 1024) continue;
         int lmax = 0;
         for (int j = 0; j < split; ++j) {
           const int l =
@@ -400,40 +429,60 @@ int launch_m1d(I8Args a, hipStream_t s) {
         const double cost = (double)((ngmax + bstep - 1) / bstep) * (lmax * (rb == 1 ? 1.0 : 1.7) + 1.0);
         if (cost < best - 1e-9) best = cost, best_split = split, best_nwv = nwv, best_rb = rb;
       }
+    }
   if (best > 1e29) return AK_INVALID;
-  const size_t smem = x_bytes + (size_t)nbmax * m1d_block_bytes(a.P, best_split) + 16;
-  switch (best_split * 10 + best_rb) {
-    case 11: launch_split<BITS, 1, 1>(a, grid, best_nwv, smem, s); break;
-    case 21: launch_split<BITS, 2, 1>(a, grid, best_nwv, smem, s); break;
-    case 41: launch_split<BITS, 4, 1>(a, grid, best_nwv, smem, s); break;
-    case 81: launch_split<BITS, 8, 1>(a, grid, best_nwv, smem, s); break;
-    case 12: launch_split<BITS, 1, 2>(a, grid, best_nwv, smem, s); break;
-    case 22: launch_split<BITS, 2, 2>(a, grid, best_nwv, smem, s); break;
-    case 42: launch_split<BITS, 4, 2>(a, grid, best_nwv, smem, s); break;
-    default: launch_split<BITS, 8, 2>(a, grid, best_nwv, smem, s); break;
+  const size_t smem = x_bytes + (size_t)nbmax * m1d_block_bytes(a.P, best_split, MT) + 16;
+  if constexpr (MT == 1) {
+    switch (best_split * 10 + best_rb) {
+      case 11: launch_split<BITS, 1, 1, 1>(a, grid, best_nwv, smem, s); break;
+      case 21: launch_split<BITS, 2, 1, 1>(a, grid, best_nwv, smem, s); break;
+      case 41: launch_split<BITS, 4, 1, 1>(a, grid, best_nwv, smem, s); break;
+      case 81: launch_split<BITS, 8, 1, 1>(a, grid, best_nwv, smem, s); break;
+      case 12: launch_split<BITS, 1, 2, 1>(a, grid, best_nwv, smem, s); break;
+      case 22: launch_split<BITS, 2, 2, 1>(a, grid, best_nwv, smem, s); break;
+      case 42: launch_split<BITS, 4, 2, 1>(a, grid, best_nwv, smem, s); break;
+      default: launch_split<BITS, 8, 2, 1>(a, grid, best_nwv, smem, s); break;
+    }
+  } else {
+    switch (best_split) {
+      case 1: launch_split<BITS, 1, 1, MT>(a, grid, best_nwv, smem, s); break;
+      case 2: launch_split<BITS, 2, 1, MT>(a, grid, best_nwv, smem, s); break;
+      case 4: launch_split<BITS, 4, 1, MT>(a, grid, best_nwv, smem, s); break;
+      default: launch_split<BITS, 8, 1, MT>(a, grid, best_nwv, smem, s); break;
+    }
   }
   return (int)hipGetLastError();
 }
 
 }  // namespace
 
-// one token; each segment's rows are processed in 4-row blocks (the last one padded).  Returns AK_INVALID if the shape
-// does not suit the kernel (group 64, activations beyond the LDS, a segment beyond 2 GB): the caller falls back to the
-// any-m kernel.
-int i8_gemv_m1(int bits, const void* x, const Segs& g, int k, int group, hipStream_t s) {
-  if (group != kG) return AK_INVALID;
+// up to 8 tokens (padded to 1, 2, 4 or 8 in the kernel); each segment's rows are processed in 4-row blocks (the last
+// one padded).  Returns AK_INVALID if the shape does not suit the kernel (group 64, the tokens' activations beyond the
+// LDS, a segment beyond 2 GB): the caller falls back to the any-m kernel.
+int i8_gemv_m1(int bits, const void* x, int m, const Segs& g, int k, int group, hipStream_t s) {
+  if (group != kG || m < 1 || m > 8) return AK_INVALID;
   I8Args a;
   a.segs = g;
   a.x = static_cast<const uint16_t*>(x);
-  a.m = 1;
+  a.m = m;
   a.k = k;
   a.nquad = kpad(k) / kG / 4;
   a.P = a.nquad < 8 ? a.nquad : 8;
   a.nb = 0;
-  switch (bits) {
-    case 4: return launch_m1d<4>(a, s);
-    case 3: return launch_m1d<3>(a, s);
-    case 2: return launch_m1d<2>(a, s);
+  const int mt = m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8;
+  switch (bits * 10 + mt) {
+    case 41: return launch_m1d<4, 1>(a, s);
+    case 31: return launch_m1d<3, 1>(a, s);
+    case 21: return launch_m1d<2, 1>(a, s);
+    case 42: return launch_m1d<4, 2>(a, s);
+    case 32: return launch_m1d<3, 2>(a, s);
+    case 22: return launch_m1d<2, 2>(a, s);
+    case 44: return launch_m1d<4, 4>(a, s);
+    case 34: return launch_m1d<3, 4>(a, s);
+    case 24: return launch_m1d<2, 4>(a, s);
+    case 48: return launch_m1d<4, 8>(a, s);
+    case 38: return launch_m1d<3, 8>(a, s);
+    case 28: return launch_m1d<2, 8>(a, s);
     default: return AK_INVALID;
   }
 }
