@@ -12,9 +12,9 @@
 //     sum(d_j * n) - OFF * sum(d_j) (the second term from the same activation operand against a constant -OFF
 //     operand), i.e. the exact integer limb sums of sum(d_j * q); GS = combined exactly in fp64;
 //     gs = fp32_rn(GS * 2^(E - 148));
-//   groups are taken in quads (4 consecutive groups, slot s = g % 4) and quads in P = min(8, #quads) contiguous
-//     stripes (stripe p = quads [p * nquad / P, (p + 1) * nquad / P)); acc[p][s] = fmaf(gs, scale, acc[p][s]) over a
-//     stripe's quads in order;
+//   groups are taken in quads (4 consecutive groups, slot s = g % 4) and the 1024-input tiles in P = min(8, #tiles)
+//     contiguous stripes (stripe p = tiles [p * nt / P, (p + 1) * nt / P)); acc[p][s] = fmaf(gs, scale, acc[p][s])
+//     over a stripe's quads in order;
 //     part[p] = ((acc[p][0] + acc[p][1]) + acc[p][2]) + acc[p][3]; y = part[0] + part[1] + ... left to right; bf16 RN.
 // The group sums are exact, so every kernel shape (token count, segmentation, row grouping, bit width of the same
 // values) gives the same bits; only the fixed fp32 order above rounds.
@@ -55,7 +55,7 @@ __device__ __forceinline__ void convert_batch(const I8Args& a, int p, int i0, in
     const int u = base + lane / LPU;
     const bool live = u < units;
     const int qi = live ? u / (4 * m) : 0, rem = live ? u % (4 * m) : 0, gq = rem / m, j = rem % m;
-    const int kk = ((stripe_begin(p, a.nquad, a.P) + i0 + qi) * 4 + gq) * G + 8 * sub;
+    const int kk = ((stripe_begin(p, a.nquad, a.P, a.qpt) + i0 + qi) * 4 + gq) * G + 8 * sub;
     uint4 v = make_uint4(0u, 0u, 0u, 0u);
     if (live && kk < k) v = *reinterpret_cast<const uint4*>(a.x + (size_t)j * k + kk);
     uint32_t t0[8], t1[8], t2[8];
@@ -160,9 +160,9 @@ __global__ void __launch_bounds__(64 * SW * RW, WPE) i8_gemv_kernel(const I8Args
 
   for (int p0 = 0; p0 < P; p0 += SW) {
     const int p = p0 + sw;
-    const int q0 = p < P ? stripe_begin(p, a.nquad, P) : 0;
-    const int nq = p < P ? stripe_begin(p + 1, a.nquad, P) - q0 : 0;
-    const int nq_round = (a.nquad + P - 1) / P;  // no stripe has more quads
+    const int q0 = p < P ? stripe_begin(p, a.nquad, P, a.qpt) : 0;
+    const int nq = p < P ? stripe_begin(p + 1, a.nquad, P, a.qpt) - q0 : 0;
+    const int nq_round = a.qpt * ((a.nquad / a.qpt + P - 1) / P);  // no stripe has more quads
     for (int i0 = 0; i0 < nq_round; i0 += nb) {
       const int nbq = nq - i0 < nb ? nq - i0 : nb;  // <= 0 when this wave's stripe has no quad here
       const bool last_batch = i0 + nb >= nq;
@@ -288,7 +288,7 @@ int launch_i8(I8Args a, hipStream_t s) {
   const size_t per_q = lds_per_quad(G, a.m);
   const size_t part_bytes = (size_t)a.P * ROWS * a.m * 4;
   const size_t accs_bytes = (size_t)SW * RW * R * NP * 4 * 64 * 4;
-  const int max_q = (a.nquad + a.P - 1) / a.P;
+  const int max_q = a.qpt * ((a.nquad / a.qpt + a.P - 1) / a.P);
   int nb = (int)((kLdsBudget - part_bytes) / (SW * per_q));
   if (nb > max_q) nb = max_q;
   if (nb < 1) return AK_INVALID;
@@ -322,7 +322,8 @@ int i8_gemv(int bits, const void* x, int m, const Segs& g, int k, int group, hip
   a.m = m;
   a.k = k;
   a.nquad = kpad(k) / group / 4;
-  a.P = a.nquad < 8 ? a.nquad : 8;
+  a.qpt = 256 / group;
+  a.P = stripe_count(a.nquad, a.qpt);
   a.nb = 1;
   switch (bits * 1000 + group) {
     case 4128: return i8_shape<4, 128>(a, s);

@@ -10,12 +10,16 @@ struct I8Args {
   const uint16_t* x;
   int m, k;
   int nquad, P;   // quads of the padded k, stripes
+  int qpt;        // quads per 1024-input tile (2 for group 128, 4 for group 64)
   int nb;         // quads per LDS batch (any-m kernel)
   int wg_end[4];  // m = 1 kernel: workgroups of segments 0..i (each workgroup serves one segment)
 };
 
-// first quad of stripe p: the P stripes are contiguous runs of quads, stripe p = [p * nquad / P, (p + 1) * nquad / P)
-__host__ __device__ inline int stripe_begin(int p, int nquad, int P) { return p * nquad / P; }
+// Stripes are contiguous runs of whole 1024-input tiles: with nt = nquad / qpt tiles, P = min(8, nt) stripes and stripe
+// p = tiles [p * nt / P, (p + 1) * nt / P), i.e. quads [qpt * (p * nt / P), qpt * ((p + 1) * nt / P)).
+__host__ __device__ inline int stripe_count(int nquad, int qpt) { return nquad / qpt < 8 ? nquad / qpt : 8; }
+// first quad of stripe p
+__host__ __device__ inline int stripe_begin(int p, int nquad, int P, int qpt) { return qpt * (p * (nquad / qpt) / P); }
 
 namespace {
 

@@ -1,33 +1,38 @@
-// The default-numerics GEMV for one token (decode, M = 1), group 128, on gfx950: the same exact integer group sums and
-// the same fp32 combine order as wq_i8.hip (rows are bit-identical to any-m launches), with an MFMA layout chosen so
-// that every weight load instruction reads whole cache lines.
+// The default-numerics GEMV for up to 8 tokens (decode and small M), group 128, on gfx950: the same exact integer
+// group sums and the same fp32 combine order as wq_i8.hip (rows are bit-identical to any-m launches), with an MFMA
+// layout chosen so that every weight load instruction reads whole cache lines.
 //
 // "Diagonal" layout of v_mfma_i32_16x16x64_i8 for a block of 4 output rows and one quad (4 groups = 16 lane chunks):
 //   lane (c, h) = (lane % 16, lane / 16);
 //   B column c = (row c >> 2 of the block, group c & 3 of the quad): lane (c, h) holds chunk 4 * (c & 3) + h of that
-//     row, so the 16 lanes of one row read its 16 consecutive chunks and one load instruction covers 4 rows x 256 B
-//     (W4; W2 and the W3 two-bit planes 128 B, the W3 third-bit plane 64 B);
+//     row;
 //   A row c = (group c >> 2, limb c & 3): lane (c, h) holds limb c & 3 of the inputs of chunk 4 * (c >> 2) + h
 //     (limb 3 is zero);
 //   D[4g + j][4r + v] is the limb-j sum of row r with the inputs of group g; only g == v is used ("the diagonal"):
 //     lane (c, h) with (c & 3) == h holds group h of row c >> 2 in its accumulators (limbs 0..2).
 // The MFMA work per weight is the same as a 16-row layout (13 of 16 A rows or columns are wasted either way), but the
-// loads are line-sized (a load pattern of 16-byte pieces 64 bytes apart reaches only about half the HBM bandwidth),
-// the A operand has 12 useful rows instead of 3, and row blocks are 4 rows, so work divides evenly over 256 CUs for
-// the decode shapes.
+// A operand has 12 useful rows instead of 3, and row blocks are 4 rows, so work divides evenly over 256 CUs.
+//
+// Items are tiles: 4 rows x one 1024-input tile (two quads), the whole of those rows' tile records, so every load
+// instruction covers whole 128-byte lines at once (a quad of a W3 record is half of each of its lines, and loads
+// of half lines reach about 4.4 TB/s against 6.5 for whole ones).  W4: one 16-byte load per quad (4 rows x 256 B).
+// W2 and the W3 two-bit planes: one 16-byte load covers both quads: lane (c, h) reads the chunk pair {2 (h >> 1),
+// 2 (h >> 1) + 1} of group (c & 3) + 4 (h & 1); one v_permlane16_swap per dword pair (odd 16-lane rows of the first
+// operand <-> even rows of the second) then leaves the quad-0 diagonal operand in the first and the quad-1 operand
+// in the second.  The W3 third-bit plane: one 8-byte load of the same chunk pair, swapped the same way.
 //
 // Work decomposition: one persistent workgroup per CU owns a contiguous range of 4-row blocks of one segment.  Its
 // tasks are (block, stripe set j < SPLIT) pairs: stripe set j = the contiguous stripes [j P / SPLIT, (j + 1) P / SPLIT),
-// i.e. a contiguous run of quads, walked in order (the fp32 order of the numerics).  Wave w always takes stripe set
+// i.e. a contiguous run of tiles, walked in order (the fp32 order of the numerics).  Wave w always takes stripe set
 // w % SPLIT, for the blocks w / SPLIT, w / SPLIT + nwv / SPLIT, ...  With SPLIT = 1 a wave owns whole blocks and adds
 // the stripe partials itself; otherwise the partials meet in LDS and the last task of a block to finish (LDS ticket)
 // adds them in stripe order.
 //
-// Item pipeline: every wave streams its items (one quad of one block: one buffer load per lane, two for W3, plus one
-// for the scales) through DEPTH register buffers.  A group of DEPTH items is one branch-free block of code, so the
-// compiler interleaves the unpacking, LDS reads and MFMAs of neighbouring items: the load offsets are a fixed per-lane
-// part plus a scalar part of (block, quad), the cursors advance by selects, and a stripe that ends inside the group
-// only leaves a copy of its accumulators; the group's epilogue turns those into stripe partials.
+// Item pipeline: every wave streams its items through DEPTH register buffers.  A group of DEPTH items is one
+// branch-free block of code, so the compiler interleaves the unpacking, LDS reads and MFMAs of neighbouring items:
+// the load offsets are a fixed per-lane part plus a scalar part of (block, tile), the cursors advance by selects,
+// and a stripe that ends inside the group only leaves a copy of its accumulators; the group's epilogue turns those
+// into stripe partials.
 #include "agens_kernels.h"
 #include "wq_common.h"
 #include "wq_i8_common.h"
@@ -37,6 +42,11 @@
 #define AK_M1_STAMP(i)
 #define AK_M1_STAMP_AFTER(i, v)
 #define AK_M1_STAMP_ITEM(i)
+#endif
+
+// tile items in flight per wave (register buffers) for one or two tokens
+#ifndef AK_M1_TILES
+#define AK_M1_TILES 2
 #endif
 
 namespace agq {
@@ -49,11 +59,41 @@ constexpr int kG = 128, kCPQ = 16;
 constexpr int kRsrcWord3 = 0x00020000;  // raw buffer resource, dword 3 (CDNA)
 constexpr int kNt = 2;                    // streaming (non-temporal) cache policy for the weights
 
+// one tile item of one lane: the raw weight words of both quads (before the W2 / W3 lane exchange) and the dwords
+// holding the two quads' scales
 template <int BITS>
-struct Rec {
-  static constexpr int bytes = 128 * BITS;          // one row's 1024-input tile
-  static constexpr int chunk = BITS == 4 ? 16 : 8;  // bytes of a lane chunk (W3: its two-bit planes)
-};
+struct TileRaw;
+template <>
+struct TileRaw<4> { uint4 q0, q1; uint32_t s0, s1; };
+template <>
+struct TileRaw<3> { uint4 lo; uint2 hi; uint32_t s0, s1; };
+template <>
+struct TileRaw<2> { uint4 lo; uint32_t s0, s1; };
+
+// v_permlane16_swap: .x = a with its odd 16-lane rows replaced by the even rows of b, .y = b with its even rows
+// replaced by the odd rows of a
+__device__ __forceinline__ uint2 swap16(uint32_t a, uint32_t b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(a, b, false, false);
+  return make_uint2(r[0], r[1]);
+}
+
+// the per-quad raw operands of a tile item (quad 0 -> r0, quad 1 -> r1)
+template <int BITS>
+__device__ __forceinline__ void split_tile(const TileRaw<BITS>& t, Raw<BITS>& r0, Raw<BITS>& r1) {
+  if constexpr (BITS == 4) {
+    r0.w = t.q0;
+    r1.w = t.q1;
+  } else {
+    const uint2 a = swap16(t.lo.x, t.lo.z), b = swap16(t.lo.y, t.lo.w);
+    r0.lo = make_uint2(a.x, b.x);
+    r1.lo = make_uint2(a.y, b.y);
+    if constexpr (BITS == 3) {
+      const uint2 hh = swap16(t.hi.x, t.hi.y);
+      r0.hi = hh.x;
+      r1.hi = hh.y;
+    }
+  }
+}
 
 // segment field i (i < 4, wave-uniform) by constant-index selects: indexing the kernel-argument arrays dynamically
 // makes the compiler hold their address in vector registers
@@ -64,12 +104,13 @@ __device__ __forceinline__ T pick4(int i, T v0, T v1, T v2, T v3) {
 #define AK_PICK(i, arr) pick4((i), (arr)[0], (arr)[1], (arr)[2], (arr)[3])
 static_assert(kMaxSegs == 4, "segment selects cover four segments");
 
-template <int BITS, int SPLIT, int DEPTH, int RB, int MT>
+template <int BITS, int SPLIT, int DEPTH, int MT>
 __global__ void __launch_bounds__(1024, 1) i8_m1d_kernel(const I8Args a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   constexpr int LPU = kG / 8, UPW = 64 / LPU, XB = 4;
-  constexpr int REC = Rec<BITS>::bytes, CHB = Rec<BITS>::chunk;
+  constexpr int REC = 128 * BITS;  // one row's tile record
   const int P = a.P, nquad = a.nquad, k = a.k, mm = a.m;  // mm <= MT tokens (the others are zero, not written)
+  const int ntile = nquad >> 1;
   const int nwv = blockDim.x >> 6;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -129,71 +170,72 @@ __global__ void __launch_bounds__(1024, 1) i8_m1d_kernel(const I8Args a) {
   for (int b = 0; b < XB; ++b) asm volatile("" ::"v"(xv[b].x), "v"(xv[b].y), "v"(xv[b].z), "v"(xv[b].w));
   AK_M1_STAMP(1);
 
-  // ---- this wave's tasks: stripe set j, quads [qa, qb), block groups b0w, b0w + bstep, ... < ng (a group is RB
-  // consecutive blocks: an item loads the same quad of each, and they share its activation operand)
-  const int ng = (nb + RB - 1) / RB;
+  // ---- this wave's tasks: stripe set j, tiles [ta, tb), blocks b0w, b0w + bstep, ... < nb
   const int j = wave % SPLIT, bstep = nwv / SPLIT, b0w = wave / SPLIT;
   const int pa = j * P / SPLIT, pb = (j + 1) * P / SPLIT;
-  const int qa = stripe_begin(pa, nquad, P), qb = stripe_begin(pb, nquad, P);
-  const int ntw = b0w < ng ? (ng - b0w + bstep - 1) / bstep : 0;
-  const int nitems = ntw * (qb - qa);
-  // bit q - qa set when quad q is the last of its stripe (quads < qa + 128)
+  const int ta = stripe_begin(pa, nquad, P, 2) >> 1, tb = stripe_begin(pb, nquad, P, 2) >> 1;
+  const int ntw = b0w < nb ? (nb - b0w + bstep - 1) / bstep : 0;
+  const int nitems = ntw * (tb - ta);
+  // bit t - ta set when tile t is the last of its stripe (tiles < ta + 128)
   unsigned long long ends0 = 0, ends1 = 0;
   for (int p = pa; p < pb; ++p) {
-    const int r = stripe_begin(p + 1, nquad, P) - 1 - qa;
+    const int r = (stripe_begin(p + 1, nquad, P, 2) >> 1) - 1 - ta;
     if (r < 64) ends0 |= 1ull << r;
     else ends1 |= 1ull << (r - 64);
   }
 
   // ---- weight addressing: per lane fixed, per item scalar.  Rows past the segment's end (padding of the last block)
   // read other rows or, past the buffer, zeros; their results are not written.
-  const int tiles = kpad(k) >> 10;
   const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<void*>(AK_PICK(sg, sgs.wt)), (short)0, tiles * n * REC, kRsrcWord3);
+      const_cast<void*>(AK_PICK(sg, sgs.wt)), (short)0, ntile * n * REC, kRsrcWord3);
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(AK_PICK(sg, sgs.st)), (short)0, tiles * n * 16, kRsrcWord3);
-  const int ch = 4 * vv + h;  // this lane's chunk within the 16 of a quad
-  const int vo_w = rr * REC + ch * CHB, vo_h = rr * REC + 256 + ch * 4, vo_s = rr * 16 + (vv & 2) * 2;
+      const_cast<uint16_t*>(AK_PICK(sg, sgs.st)), (short)0, ntile * n * 16, kRsrcWord3);
+  // W4: chunk 4 vv + h of each quad; W2 / W3: the chunk pair of group vv + 4 (h & 1) starting at chunk 2 (h >> 1)
+  const int cp = 4 * (vv + 4 * (h & 1)) + 2 * (h >> 1);
+  const int vo_w = rr * REC + (BITS == 4 ? (4 * vv + h) * 16 : cp * 8), vo_h = rr * REC + 256 + cp * 4;
+  const int vo_s = rr * 16 + (vv & 2) * 2;
   const int tile_w = n * REC, tile_s = n * 16;
-  auto fetch1 = [&](int blk, int qd, Raw<BITS>& dst, uint32_t& sdst) {
+  auto fetch = [&](int blk, int t, TileRaw<BITS>& d) {
     const int row0 = (b_lo + blk) * 4;
-    const int so = row0 * REC + (qd >> 1) * tile_w, odd = qd & 1;
+    const int so = row0 * REC + t * tile_w;
     if constexpr (BITS == 4) {
-      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rw, vo_w, so + odd * 256, kNt);
-      dst.w = make_uint4(v[0], v[1], v[2], v[3]);
+      const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(rw, vo_w, so, kNt);
+      const u32x4 v1 = __builtin_amdgcn_raw_buffer_load_b128(rw, vo_w, so + 256, kNt);
+      d.q0 = make_uint4(v0[0], v0[1], v0[2], v0[3]);
+      d.q1 = make_uint4(v1[0], v1[1], v1[2], v1[3]);
     } else {
-      typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-      const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rw, vo_w, so + odd * 128, kNt);
-      dst.lo = make_uint2(v[0], v[1]);
-      if constexpr (BITS == 3) dst.hi = __builtin_amdgcn_raw_buffer_load_b32(rw, vo_h, so + odd * 64, kNt);
+      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rw, vo_w, so, kNt);
+      d.lo = make_uint4(v[0], v[1], v[2], v[3]);
+      if constexpr (BITS == 3) {
+        typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+        const u32x2 g = __builtin_amdgcn_raw_buffer_load_b64(rw, vo_h, so, kNt);
+        d.hi = make_uint2(g[0], g[1]);
+      }
     }
-    // the aligned dword holding the scale (the item selects its half): a 16-bit value would be widened or packed at
-    // the loop latch, which waits for the load
-    sdst = __builtin_amdgcn_raw_buffer_load_b32(rs, vo_s, row0 * 16 + (qd >> 1) * tile_s + odd * 8, 0);
-  };
-  auto fetch = [&](int grp, int qd, Raw<BITS> (&dst)[RB], uint32_t (&sdst)[RB]) {
-#pragma unroll
-    for (int r = 0; r < RB; ++r) fetch1(grp * RB + r, qd, dst[r], sdst[r]);
+    // the aligned dwords holding the scales (the item selects the halves): a 16-bit value would be widened or packed
+    // at the loop latch, which waits for the load
+    const int ss = row0 * 16 + t * tile_s;
+    d.s0 = __builtin_amdgcn_raw_buffer_load_b32(rs, vo_s, ss, 0);
+    d.s1 = __builtin_amdgcn_raw_buffer_load_b32(rs, vo_s, ss + 8, 0);
   };
 
-  Raw<BITS> buf[DEPTH][RB];
-  uint32_t sbuf[DEPTH][RB];
+  TileRaw<BITS> buf[DEPTH];
 
-  // fetch cursor (an item past the end reloads quad qa of block 0: cache-resident, never used, and the load sequence
+  // fetch cursor (an item past the end reloads tile ta of block 0: cache-resident, never used, and the load sequence
   // stays branch-free so the compiler's load counters stay exact)
-  int fb = b0w, fq = qa;
-  auto fetch_next = [&](Raw<BITS> (&dst)[RB], uint32_t (&sdst)[RB]) {
-    const bool in = fb < ng;
-    fetch(in ? fb : 0, in ? fq : qa, dst, sdst);
-    const bool wrap = fq + 1 == qb;
-    fq = wrap ? qa : fq + 1;
+  int fb = b0w, ft = ta;
+  auto fetch_next = [&](TileRaw<BITS>& dst) {
+    const bool in = fb < nb;
+    fetch(in ? fb : 0, in ? ft : ta, dst);
+    const bool wrap = ft + 1 == tb;
+    ft = wrap ? ta : ft + 1;
     fb = wrap ? fb + bstep : fb;
   };
 
   // ---- the first DEPTH items are requested, then step 2 of the activations: per group the limbs (to LDS), and in
   // meta the bias sums -OFF * sum(d_j) of the three limbs with the activation scale 2^(E - 148) as float bits
 #pragma unroll
-  for (int d = 0; d < DEPTH; ++d) fetch_next(buf[d], sbuf[d]);
+  for (int d = 0; d < DEPTH; ++d) fetch_next(buf[d]);
 
   auto convert = [&](int p0) {
 #pragma unroll
@@ -243,78 +285,73 @@ __global__ void __launch_bounds__(1024, 1) i8_m1d_kernel(const I8Args a) {
   const int r4 = 4 * (lane & 3);
   const int sl0 = 4 * r4, sl1 = 4 * (17 + r4), sl2 = 4 * (34 + r4), sl3 = 4 * (51 + r4);
 
-  // compute cursor: block, quad, stripe
-  int cb = b0w, cq = qa, cp = pa;
-  float acc[RB][MT], yrun[RB][MT];
+  // compute cursor: block, tile, stripe
+  int cb = b0w, ct = ta, cs = pa;
+  float acc[MT], yrun[MT];
 #pragma unroll
-  for (int r = 0; r < RB; ++r)
-#pragma unroll
-    for (int t = 0; t < MT; ++t) acc[r][t] = 0.f, yrun[r][t] = 0.f;
-  // one item without branches: an[][] = the accumulators before a stripe end reset them (used only at a stripe end)
-  auto core = [&](const Raw<BITS> (&bf)[RB], const uint32_t (&sraw)[RB], float (&an)[RB][MT], bool& end, int& eg,
-                  int& ep) {
-    const int r0 = cq - qa;
+  for (int t = 0; t < MT; ++t) acc[t] = 0.f, yrun[t] = 0.f;
+  // one item without branches: an[] = the accumulators before a stripe end reset them (used only at a stripe end)
+  auto core = [&](const TileRaw<BITS>& bf, float (&an)[MT], bool& end, int& eg, int& ep) {
+    const int r0 = ct - ta;
     end = ((r0 < 64 ? ends0 >> r0 : ends1 >> (r0 - 64)) & 1ull) != 0;
-    i32x4 b0[RB], b1[RB];
-    float sc[RB];
+    Raw<BITS> rq[2];
+    split_tile<BITS>(bf, rq[0], rq[1]);
 #pragma unroll
-    for (int r = 0; r < RB; ++r) {
-      sc[r] = __uint_as_float(__builtin_amdgcn_perm(sraw[r], sraw[r], ssel));
-      make_b<BITS>(bf[r], b0[r], b1[r]);
-    }
-    // token by token: the activation operand and meta of one token are live at a time
-#pragma unroll
-    for (int t = 0; t < MT; ++t) {
-      const i32x4 mt = meta[(t * nquad + cq) * 4 + h];
-      const uint8_t* src = lds + a_base + t * a_tmul + cq * a_qmul;
-      const i32x4 a0 = *reinterpret_cast<const i32x4*>(src);
-      const i32x4 a1 = *reinterpret_cast<const i32x4*>(src + (a_on ? kCPQ * 48 : 0));
-#pragma unroll
-      for (int r = 0; r < RB; ++r) {
-        i32x4 d = mt;
-        d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0[r], d, 0, 0, 0);
-        d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1[r], d, 0, 0, 0);
-        an[r][t] = fmaf(group_sum_f32(d), sc[r] * __int_as_float(mt[3]), acc[r][t]);
-        acc[r][t] = end ? 0.f : an[r][t];
-      }
-    }
-    eg = cb;
-    ep = cp;
-    cp = end ? cp + 1 : cp;
-    const bool wrap = cq + 1 == qb;
-    cq = wrap ? qa : cq + 1;
-    cb = wrap ? cb + bstep : cb;
-    cp = wrap ? pa : cp;
-  };
-  // a stripe ended with accumulators v[][]: its partial per row (lanes 0..3: ((slot 0 + slot 1) + slot 2) + slot 3,
-  // slot v of row r in lane 17v + 4r), then the blocks' outputs when the task ends
-  auto stripe_end = [&](const float (&v)[RB][MT], int eg, int ep) {
-    float pp[RB][MT];
-#pragma unroll
-    for (int r = 0; r < RB; ++r)
+    for (int qq = 0; qq < 2; ++qq) {
+      i32x4 b0, b1;
+      const uint32_t sraw = qq ? bf.s1 : bf.s0;
+      const float sc = __uint_as_float(__builtin_amdgcn_perm(sraw, sraw, ssel));
+      make_b<BITS>(rq[qq], b0, b1);
+      const int cq = 2 * ct + qq;
+      // token by token: the activation operand and meta of one token are live at a time
 #pragma unroll
       for (int t = 0; t < MT; ++t) {
-        const int vi = __float_as_int(v[r][t]);
-        const float v0 = __int_as_float(__builtin_amdgcn_ds_bpermute(sl0, vi)),
-                    v1 = __int_as_float(__builtin_amdgcn_ds_bpermute(sl1, vi)),
-                    v2 = __int_as_float(__builtin_amdgcn_ds_bpermute(sl2, vi)),
-                    v3 = __int_as_float(__builtin_amdgcn_ds_bpermute(sl3, vi));
-        pp[r][t] = ((v0 + v1) + v2) + v3;
+        const i32x4 mt = meta[(t * nquad + cq) * 4 + h];
+        const uint8_t* src = lds + a_base + t * a_tmul + cq * a_qmul;
+        const i32x4 a0 = *reinterpret_cast<const i32x4*>(src);
+        const i32x4 a1 = *reinterpret_cast<const i32x4*>(src + (a_on ? kCPQ * 48 : 0));
+        i32x4 d = mt;
+        d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, d, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, d, 0, 0, 0);
+        acc[t] = fmaf(group_sum_f32(d), sc * __int_as_float(mt[3]), acc[t]);
       }
+    }
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      an[t] = acc[t];
+      acc[t] = end ? 0.f : acc[t];
+    }
+    eg = cb;
+    ep = cs;
+    cs = end ? cs + 1 : cs;
+    const bool wrap = ct + 1 == tb;
+    ct = wrap ? ta : ct + 1;
+    cb = wrap ? cb + bstep : cb;
+    cs = wrap ? pa : cs;
+  };
+  // a stripe ended with accumulators v[]: its partial per row (lanes 0..3: ((slot 0 + slot 1) + slot 2) + slot 3,
+  // slot v of row r in lane 17v + 4r), then the blocks' outputs when the task ends
+  auto stripe_end = [&](const float (&v)[MT], int eg, int ep) {
+    float pp[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      const int vi = __float_as_int(v[t]);
+      const float v0 = __int_as_float(__builtin_amdgcn_ds_bpermute(sl0, vi)),
+                  v1 = __int_as_float(__builtin_amdgcn_ds_bpermute(sl1, vi)),
+                  v2 = __int_as_float(__builtin_amdgcn_ds_bpermute(sl2, vi)),
+                  v3 = __int_as_float(__builtin_amdgcn_ds_bpermute(sl3, vi));
+      pp[t] = ((v0 + v1) + v2) + v3;
+    }
     if constexpr (SPLIT == 1) {
 #pragma unroll
-      for (int r = 0; r < RB; ++r)
-#pragma unroll
-        for (int t = 0; t < MT; ++t) {
-          yrun[r][t] = ep == 0 ? pp[r][t] : yrun[r][t] + pp[r][t];
-          if (ep == P - 1 && eg * RB + r < nb) write_y(eg * RB + r, t, yrun[r][t]);
-        }
+      for (int t = 0; t < MT; ++t) {
+        yrun[t] = ep == 0 ? pp[t] : yrun[t] + pp[t];
+        if (ep == P - 1) write_y(eg, t, yrun[t]);
+      }
     } else {
 #pragma unroll
-      for (int r = 0; r < RB; ++r)
-#pragma unroll
-        for (int t = 0; t < MT; ++t)
-          if (lane < 4 && eg * RB + r < nb) part[(((eg * RB + r) * P + ep) * MT + t) * 4 + lane] = pp[r][t];
+      for (int t = 0; t < MT; ++t)
+        if (lane < 4) part[((eg * P + ep) * MT + t) * 4 + lane] = pp[t];
       if (ep + 1 < pb) return;  // more stripes in this task
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");  // LDS only: no wait for loads in flight
       int last = 0;
@@ -322,16 +359,12 @@ __global__ void __launch_bounds__(1024, 1) i8_m1d_kernel(const I8Args a) {
       last = __shfl(last, 0);
       if (last) {
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+        const float* slot = part + eg * P * MT * 4;
 #pragma unroll
-        for (int r = 0; r < RB; ++r) {
-          if (eg * RB + r >= nb) continue;
-          const float* slot = part + (eg * RB + r) * P * MT * 4;
-#pragma unroll
-          for (int t = 0; t < MT; ++t) {
-            float y = slot[t * 4 + (lane & 3)];
-            for (int q = 1; q < P; ++q) y += slot[(q * MT + t) * 4 + (lane & 3)];
-            write_y(eg * RB + r, t, y);
-          }
+        for (int t = 0; t < MT; ++t) {
+          float y = slot[t * 4 + (lane & 3)];
+          for (int q = 1; q < P; ++q) y += slot[(q * MT + t) * 4 + (lane & 3)];
+          write_y(eg, t, y);
         }
       }
     }
@@ -339,13 +372,13 @@ __global__ void __launch_bounds__(1024, 1) i8_m1d_kernel(const I8Args a) {
 
   const int nfull = nitems / DEPTH * DEPTH;
   for (int i0 = 0; i0 < nfull; i0 += DEPTH) {
-    float sv[DEPTH][RB][MT];
+    float sv[DEPTH][MT];
     bool end[DEPTH];
     int eg[DEPTH], ep[DEPTH];
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) {
-      core(buf[d], sbuf[d], sv[d], end[d], eg[d], ep[d]);
-      fetch_next(buf[d], sbuf[d]);
+      core(buf[d], sv[d], end[d], eg[d], ep[d]);
+      fetch_next(buf[d]);
     }
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d)
@@ -355,10 +388,10 @@ __global__ void __launch_bounds__(1024, 1) i8_m1d_kernel(const I8Args a) {
 #pragma unroll
   for (int d = 0; d < DEPTH; ++d) {
     if (nfull + d < nitems) {
-      float v[RB][MT];
+      float v[MT];
       bool e;
       int g, p;
-      core(buf[d], sbuf[d], v, e, g, p);
+      core(buf[d], v, e, g, p);
       if (e) stripe_end(v, g, p);
     }
   }
@@ -375,19 +408,19 @@ size_t m1d_block_bytes(int P, int split, int mt) {  // per 4-row block: outputs,
   return (size_t)mt * 8 + (split > 1 ? (size_t)P * 16 * mt + 4 : 0);
 }
 
-template <int BITS, int SPLIT, int RB, int MT>
+template <int BITS, int SPLIT, int MT>
 void launch_split(const I8Args& a, int grid, int nwv, size_t smem, hipStream_t s) {
-  constexpr int DEPTH = RB * MT <= 2 ? 4 / RB : 2;  // items in flight per wave
-  hipLaunchKernelGGL((i8_m1d_kernel<BITS, SPLIT, DEPTH, RB, MT>), dim3(grid), dim3(64 * nwv), smem, s, a);
+  constexpr int DEPTH = MT <= 2 ? AK_M1_TILES : 1;  // items in flight per wave
+  hipLaunchKernelGGL((i8_m1d_kernel<BITS, SPLIT, DEPTH, MT>), dim3(grid), dim3(64 * nwv), smem, s, a);
 }
 
 template <int BITS, int MT>
 int launch_m1d(I8Args a, hipStream_t s) {
   const Segs& g = a.segs;
   const size_t x_bytes = m1d_x_bytes(a.nquad, MT);
-  const int tiles = kpad(a.k) >> 10;
+  const int ntile = a.nquad / 2;
   for (int i = 0; i < g.nseg; ++i)  // buffer offsets are 32-bit
-    if ((long long)tiles * g.n[i] * 128 * BITS >= (1ll << 31)) return AK_INVALID;
+    if ((long long)ntile * g.n[i] * 128 * BITS >= (1ll << 31)) return AK_INVALID;
   if (x_bytes > 150 * 1024) return AK_INVALID;
   // workgroups per segment: about the same number of blocks each, at most one workgroup per CU
   int total = 0;
@@ -408,48 +441,31 @@ int launch_m1d(I8Args a, hipStream_t s) {
     const int nbs = (g.n[i] + 3) / 4, gs = (nbs + per - 1) / per;
     nbmax = (nbs + gs - 1) / gs > nbmax ? (nbs + gs - 1) / gs : nbmax;
   }
-  // waves per workgroup, waves per block and blocks per item: fewest item rounds for the busiest wave, a task's
-  // overhead counted as about one item and a two-block item as 1.7 items; ties go to more waves (latency hiding),
-  // fewer waves per block (less exchange) and single blocks (finer balance)
-  int best_split = 1, best_nwv = 16, best_rb = 1;
+  // waves per workgroup and waves per block: fewest item rounds for the busiest wave, a task's overhead counted as
+  // about half an item; ties go to more waves (latency hiding) and fewer waves per block (less exchange)
+  int best_split = 1, best_nwv = 16;
   double best = 1e30;
-  for (int rb : {1, 2})
-    for (int nwv : {16, 8}) {
-      if (MT > 1 && rb > 1) continue;
-      for (int split : {1, 2, 4, 8}) {
-        if (split > a.P) break;
-        if (x_bytes + (size_t)nbmax * m1d_block_bytes(a.P, split, MT) + 16 > 160 * 1024) continue;
-        int lmax = 0;
-        for (int j = 0; j < split; ++j) {
-          const int l =
-              stripe_begin((j + 1) * a.P / split, a.nquad, a.P) - stripe_begin(j * a.P / split, a.nquad, a.P);
-          lmax = l > lmax ? l : lmax;
-        }
-        const int bstep = nwv / split, ngmax = (nbmax + rb - 1) / rb;
-        const double cost = (double)((ngmax + bstep - 1) / bstep) * (lmax * (rb == 1 ? 1.0 : 1.7) + 1.0);
-        if (cost < best - 1e-9) best = cost, best_split = split, best_nwv = nwv, best_rb = rb;
+  for (int nwv : {16, 8})
+    for (int split : {1, 2, 4, 8}) {
+      if (split > a.P) break;
+      if (x_bytes + (size_t)nbmax * m1d_block_bytes(a.P, split, MT) + 16 > 160 * 1024) continue;
+      int lmax = 0;
+      for (int j = 0; j < split; ++j) {
+        const int l = (stripe_begin((j + 1) * a.P / split, a.nquad, a.P, 2) -
+                       stripe_begin(j * a.P / split, a.nquad, a.P, 2)) / 2;
+        lmax = l > lmax ? l : lmax;
       }
+      const int bstep = nwv / split;
+      const double cost = (double)((nbmax + bstep - 1) / bstep) * (lmax + 0.5);
+      if (cost < best - 1e-9) best = cost, best_split = split, best_nwv = nwv;
     }
   if (best > 1e29) return AK_INVALID;
   const size_t smem = x_bytes + (size_t)nbmax * m1d_block_bytes(a.P, best_split, MT) + 16;
-  if constexpr (MT == 1) {
-    switch (best_split * 10 + best_rb) {
-      case 11: launch_split<BITS, 1, 1, 1>(a, grid, best_nwv, smem, s); break;
-      case 21: launch_split<BITS, 2, 1, 1>(a, grid, best_nwv, smem, s); break;
-      case 41: launch_split<BITS, 4, 1, 1>(a, grid, best_nwv, smem, s); break;
-      case 81: launch_split<BITS, 8, 1, 1>(a, grid, best_nwv, smem, s); break;
-      case 12: launch_split<BITS, 1, 2, 1>(a, grid, best_nwv, smem, s); break;
-      case 22: launch_split<BITS, 2, 2, 1>(a, grid, best_nwv, smem, s); break;
-      case 42: launch_split<BITS, 4, 2, 1>(a, grid, best_nwv, smem, s); break;
-      default: launch_split<BITS, 8, 2, 1>(a, grid, best_nwv, smem, s); break;
-    }
-  } else {
-    switch (best_split) {
-      case 1: launch_split<BITS, 1, 1, MT>(a, grid, best_nwv, smem, s); break;
-      case 2: launch_split<BITS, 2, 1, MT>(a, grid, best_nwv, smem, s); break;
-      case 4: launch_split<BITS, 4, 1, MT>(a, grid, best_nwv, smem, s); break;
-      default: launch_split<BITS, 8, 1, MT>(a, grid, best_nwv, smem, s); break;
-    }
+  switch (best_split) {
+    case 1: launch_split<BITS, 1, MT>(a, grid, best_nwv, smem, s); break;
+    case 2: launch_split<BITS, 2, MT>(a, grid, best_nwv, smem, s); break;
+    case 4: launch_split<BITS, 4, MT>(a, grid, best_nwv, smem, s); break;
+    default: launch_split<BITS, 8, MT>(a, grid, best_nwv, smem, s); break;
   }
   return (int)hipGetLastError();
 }
@@ -467,7 +483,8 @@ int i8_gemv_m1(int bits, const void* x, int m, const Segs& g, int k, int group, 
   a.m = m;
   a.k = k;
   a.nquad = kpad(k) / kG / 4;
-  a.P = a.nquad < 8 ? a.nquad : 8;
+  a.qpt = 2;
+  a.P = stripe_count(a.nquad, a.qpt);
   a.nb = 0;
   const int mt = m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8;
   switch (bits * 10 + mt) {

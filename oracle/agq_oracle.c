@@ -342,7 +342,7 @@ void ora_gemv_fast_kt(int bits, const uint16_t* x, int m, const uint8_t* wt, con
 void ora_gemv_fast_kt_rows(int bits, const uint16_t* x, int m, const uint8_t* wt, const uint16_t* st, uint16_t* y,
                            int ldy, int n, int k, int group, int r0, int r1) {
   const int kp = kpad(k), SPT = 1024 / group, ngroups = kp / group, nquad = ngroups / 4;
-  const int P = nquad < 8 ? nquad : 8;
+  const int nt = kp / 1024, qpt = nquad / nt, P = nt < 8 ? nt : 8;
   int8_t* q = (int8_t*)malloc((size_t)kp);
   for (int o = r0; o < r1; ++o) {
     kt_row_q(bits, wt, n, k, o, q);
@@ -351,7 +351,7 @@ void ora_gemv_fast_kt_rows(int bits, const uint16_t* x, int m, const uint8_t* wt
       float acc[8][4];
       memset(acc, 0, sizeof(acc));
       for (int qd = 0, p = 0; qd < nquad; ++qd) {
-        while (qd >= (p + 1) * nquad / P) ++p; /* stripe p = quads [p * nquad / P, (p + 1) * nquad / P) */
+        while (qd >= qpt * ((p + 1) * nt / P)) ++p; /* stripe p = tiles [p * nt / P, (p + 1) * nt / P) */
         for (int s = 0; s < 4; ++s) {
           const int g = 4 * qd + s, t = g * group / 1024, gi = g % SPT;
           int E;

@@ -55,8 +55,8 @@ void ora_gemv_exact_kt(int bits, const uint16_t* x, int m, const uint8_t* wt, co
  *    balanced signed bytes x_int = d2 * 2^16 + d1 * 2^8 + d0; exact integer limb sums D_j = sum d_j * q;
  *    gsum = fmaf((float)(D2 * 256 + D1), 256, (float)D0) (= fp32_rn of the exact group dot product times 2^(148-E)
  *    unless |D2 * 256 + D1| >= 2^24); sE = scale * 2^(E-148) (fp32 multiply);
- *  - groups in quads of 4 (slot s = g % 4), quads in P = min(8, nquad) contiguous stripes (stripe p = quads
- *    [p * nquad / P, (p + 1) * nquad / P));
+ *  - groups in quads of 4 (slot s = g % 4); the nt = kpad(k) / 1024 tiles in P = min(8, nt) contiguous stripes
+ *    (stripe p = tiles [p * nt / P, (p + 1) * nt / P), i.e. whole tiles of quads);
  *    acc[p][s] = fmaf(gsum, sE, acc[p][s]) over the stripe's quads in order;
  *    part[p] = ((acc[p][0] + acc[p][1]) + acc[p][2]) + acc[p][3]; y = part[0] + part[1] + ... (left to right); bf16 RN.
  * Same semantics as reference.rs:53-71 (sum_g s_g * sum_{i in g} x_i q_i, fp32 accumulation); only the rounding
