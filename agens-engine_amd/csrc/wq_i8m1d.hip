@@ -42,6 +42,8 @@
 #define AK_M1_STAMP(i)
 #define AK_M1_STAMP_AFTER(i, v)
 #define AK_M1_STAMP_ITEM(i)
+#define AK_M1_WG_BEGIN()
+#define AK_M1_WG_END()
 #endif
 
 // tile items in flight per wave (register buffers) for one or two tokens
@@ -107,6 +109,7 @@ static_assert(kMaxSegs == 4, "segment selects cover four segments");
 template <int BITS, int SPLIT, int DEPTH, int MT>
 __global__ void __launch_bounds__(1024, 1) i8_m1d_kernel(const I8Args a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  AK_M1_WG_BEGIN();
   constexpr int LPU = kG / 8, UPW = 64 / LPU, XB = 4;
   constexpr int REC = 128 * BITS;  // one row's tile record
   const int P = a.P, nquad = a.nquad, k = a.k, mm = a.m;  // mm <= MT tokens (the others are zero, not written)
@@ -240,7 +243,7 @@ __global__ void __launch_bounds__(1024, 1) i8_m1d_kernel(const I8Args a) {
   auto convert = [&](int p0) {
 #pragma unroll
     for (int b = 0; b < XB; ++b) {
-      if (p0 + b >= npass) break;
+      if (p0 + b >= npass || wave * UPW + (p0 + b) * ustride >= units) break;  // no unit of this wave (uniform)
       const int u = u0 + (p0 + b) * ustride;
       uint32_t t0[8], t1[8], t2[8];
       const int e = group_limbs<LPU>(xv[b], t0, t1, t2);
@@ -401,6 +404,7 @@ __global__ void __launch_bounds__(1024, 1) i8_m1d_kernel(const I8Args a) {
     const int t = MT == 1 ? 0 : i / (nb * 4), row = b_lo * 4 + i - t * nb * 4;
     if (t < mm && row < n) yseg[(size_t)t * ldy + row] = yl[i];
   }
+  AK_M1_WG_END();
 }
 
 size_t m1d_x_bytes(int nquad, int mt) { return 512 + (size_t)mt * nquad * (kCPQ * 96 + 4 * 16); }
