@@ -24,6 +24,7 @@ import numpy as np
 ROOT = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.join(ROOT, "agens-engine_amd")
 HBM_PEAK_GBS = 8000.0
+INT8_PEAK_OPS = 5.0e15  # MI355X dense int8 MFMA peak (ops/s); algorithmic 2*M*n*k is counted against it
 SEED = 20261201
 
 
@@ -187,6 +188,16 @@ def build_sweep(ctx, m, cpu_layers):
     return plan, meta, cpu
 
 
+def nlin_layers(cpu, nlin):
+    """the number of leading entries of `cpu` that hold the first nlin linears"""
+    c = 0
+    for i, (_, _, lins) in enumerate(cpu):
+        c += len(lins)
+        if c >= nlin:
+            return i + 1
+    return len(cpu)
+
+
 def cpu_baseline(ctx, m, cpu, budget_s=20.0):
     """The reference's CPU path (reference.rs:53-71, restated in C by the oracle: per-group fp32 sums) on the first
     layers of the same sweep, single thread, timed on this host; GB/s of the same algorithmic bytes."""
@@ -214,7 +225,19 @@ def cpu_baseline(ctx, m, cpu, budget_s=20.0):
         bytes_total += m * k * 2
         if t_total > budget_s:
             break
+    # the same sample on all host cores (rows split statically over threads), reported beside the scalar figure
+    nthr = max(1, min(os.cpu_count() or 1, 16))
+    t_all = 0.0
+    for x, k, lins in cpu[:nlin_layers(cpu, nlin)]:
+        xh = xs[(x.value, k)]
+        for lin in lins:
+            p, s = lin.container
+            y = np.zeros(m * lin.n, dtype=np.float32)
+            t0 = time.perf_counter()
+            O.ora_gemv_ref_f32(ptr(xh), m, ptr(p), ptr(s), ptr(y), lin.n, lin.n, k, 128, nthr)
+            t_all += time.perf_counter() - t0
     return {"value": round(bytes_total / t_total / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "all_cores": {"value": round(bytes_total / t_all / 1e9, 3), "cores": nthr},
             "sample": f"{nlin} linears of the sweep's first layers (M={m}), reference CPU path restated in C "
                       f"(oracle/agq_oracle.c ora_gemv_ref_f32, reference.rs:53-71), {t_total:.1f} s"}
 
@@ -291,7 +314,7 @@ def run_single(args, K, B):
     ctx = Ctx(K, B)
     cfgs = {0: [(4, [5120], 5120, 1.0)], 1: [(3, [55296], 5120, 1.0)], 2: [(2, [5120], 27648, 0.5)],
             3: [(4, [5120, 1024, 1024], 5120, 1.0), (4, [5120], 5120, 1.0)]}
-    ms_list = [args.m] if args.config != 3 else [2, 4, 8, 16] if args.m == 1 else [args.m]
+    ms_list = [args.m] if args.config != 3 else [1, 2, 4, 8, 16] if args.m == 1 else [args.m]
     lines = []
     for bits, ns, k, xs in cfgs[args.config]:
         for m in ms_list:
@@ -308,9 +331,12 @@ def run_single(args, K, B):
             ctx.check(B.agb_run(arr, len(plan), args.warmup, steps, 0 if args.eager else 1, ctypes.byref(t)), "run")
             us = t.value * 1e3 / copies
             by = algo_bytes(plan[0])
+            flops = 2.0 * m * sum(ns) * k  # algorithmic multiply-adds x 2
             lines.append({"config": args.config, "bits": bits, "n": ns, "k": k, "m": m, "us": round(us, 2),
                           "GBps": round(by / (us * 1e-6) / 1e9, 1), "pct_of_peak": round(100 * by / (us * 1e-6) / 1e9
                                                                                          / HBM_PEAK_GBS, 2),
+                          "TOPS": round(flops / (us * 1e-6) / 1e12, 2),
+                          "mfma_util_int8": round(flops / (us * 1e-6) / INT8_PEAK_OPS, 5),
                           "bytes": by, "copies": copies, "graph": not args.eager})
             ctx.free_all()
     return lines
