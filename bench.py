@@ -253,27 +253,21 @@ def run_sweep(args, K, B):
     ctx.check(B.agb_run(arr, len(plan), args.warmup, args.steps, 0 if args.eager else 1, ctypes.byref(ms)), "run")
     total_bytes = sum(algo_bytes(L) for L in plan)
     gbs = total_bytes / (ms.value * 1e-3) / 1e9
-    # per-launch durations (events around every launch) -> the dominant kernel
-    each = (ctypes.c_float * len(plan))()
-    ctx.check(B.agb_time_each(arr, len(plan), 3, each), "time each")
-    # the dominant kernel: the launch class (linear, bit width; one kernel instance per shape) with the most time
+    # per launch class (linear, bit width; one kernel instance per shape): its launches of the sweep replayed alone
+    # as one graph, back to back like in the sweep; the class with the most time is the dominant kernel
+    classes = {}
+    for L, (name, b) in zip(plan, meta):
+        classes.setdefault(f"{name}_w{b}", []).append(L)
     by_kernel = {}
-    for L, (name, b), t in zip(plan, meta, each):
-        key = f"{name}_w{b}"
-        d = by_kernel.setdefault(key, {"ms": 0.0, "bytes": 0, "launches": 0})
-        d["ms"] += t
-        d["bytes"] += algo_bytes(L)
-        d["launches"] += 1
+    for key, ls in classes.items():
+        sub = (AgbLaunch * len(ls))(*ls)
+        t = ctypes.c_float()
+        ctx.check(B.agb_run(sub, len(ls), 1, 5, 0 if args.eager else 1, ctypes.byref(t)), "class run")
+        by_kernel[key] = {"ms": t.value, "bytes": sum(algo_bytes(L) for L in ls), "launches": len(ls)}
     dom_name, dom = max(by_kernel.items(), key=lambda kv: kv[1]["ms"])
     achieved = dom["bytes"] / (dom["ms"] * 1e-3) / 1e9
-    per_type = {}
-    for L, (name, b), t in zip(plan, meta, each):
-        d = per_type.setdefault(f"{name}_w{b}", {"us": 0.0, "bytes": 0, "n": 0})
-        d["us"] += t * 1e3
-        d["bytes"] += algo_bytes(L)
-        d["n"] += 1
-    detail = {k: {"launches": v["n"], "us_each": round(v["us"] / v["n"], 2),
-                  "GBps": round(v["bytes"] / (v["us"] * 1e-6) / 1e9, 1)} for k, v in sorted(per_type.items())}
+    detail = {k: {"launches": v["launches"], "us_each": round(v["ms"] * 1e3 / v["launches"], 2),
+                  "GBps": round(v["bytes"] / (v["ms"] * 1e-3) / 1e9, 1)} for k, v in sorted(by_kernel.items())}
     read_bw = ctypes.c_float()
     ctx.check(B.agb_read_bw(4 << 30, 5, ctypes.byref(read_bw)), "read bw")
     cpu_res = cpu_baseline(ctx, args.m, cpu) if cpu else None
