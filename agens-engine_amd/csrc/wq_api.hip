@@ -16,6 +16,7 @@ int exact_gemv(int bits, const void* x, int m, const Segs& g, int k, int group, 
 int exact_ct_gemv(const void* x, const int32_t* packed, const void* scales, void* y, int n, int k, hipStream_t s);
 int i8_gemv(int bits, const void* x, int m, const Segs& g, int k, int group, hipStream_t s);
 int i8_gemv_m1(int bits, const void* x, int m, const Segs& g, int k, int group, hipStream_t s);
+int i8_gemv_mt(int bits, const void* x, int m, const Segs& g, int k, int group, hipStream_t s);
 
 namespace {
 
@@ -52,8 +53,9 @@ Segs make_segs(int nseg, const void* const* wt, const void* const* st, void* con
   return g;
 }
 
-// the default path for m <= 16 tokens: the line-load kernel (wq_i8m1d.hip) for up to 8 tokens at a time when the
-// tokens' activations fit its LDS, otherwise the any-m kernel (wq_i8.hip)
+// the default path for m <= 16 tokens, in chunks of at most 8: the tokens-in-A-rows kernel (wq_i8mt.hip) for 3..8
+// tokens and the line-load kernel (wq_i8m1d.hip) for one or two (or where the first does not fit) when the tokens'
+// activations fit the LDS, otherwise the any-m kernel (wq_i8.hip)
 int run_i8(int bits, const void* x, int m, const Segs& g, int k, int group, hipStream_t s) {
   const int mt = m <= 8 ? m : (m + 1) / 2;
   bool ok = true;
@@ -61,7 +63,9 @@ int run_i8(int bits, const void* x, int m, const Segs& g, int k, int group, hipS
     const int mm = m - m0 < mt ? m - m0 : mt;
     Segs gg = g;
     for (int i = 0; i < g.nseg; ++i) gg.y[i] = g.y[i] + (size_t)m0 * g.ldy[i];
-    const int e = i8_gemv_m1(bits, static_cast<const uint16_t*>(x) + (size_t)m0 * k, mm, gg, k, group, s);
+    const void* xx = static_cast<const uint16_t*>(x) + (size_t)m0 * k;
+    int e = mm >= 3 ? i8_gemv_mt(bits, xx, mm, gg, k, group, s) : AK_INVALID;  // measured: 2 tokens faster below
+    if (e == AK_INVALID) e = i8_gemv_m1(bits, xx, mm, gg, k, group, s);
     if (e == AK_INVALID && m0 == 0) {
       ok = false;
     } else if (e) {

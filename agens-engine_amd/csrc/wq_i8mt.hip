@@ -1,0 +1,469 @@
+// The default-numerics GEMV for 3..8 tokens (speculative verify, small batches), group 128, on gfx950: the same exact
+// integer group sums and the same fp32 combine order as wq_i8.hip / wq_i8m1d.hip (every output row is bit-identical
+// to its one-token launch), with the tokens in the rows of the MFMA A operand: one v_mfma_i32_16x16x64_i8 serves
+// 4 tokens x 16 output rows instead of 1 token x 4 rows.
+//
+// MFMA layout (16-row blocks, one group of 128 inputs per pair of MFMAs):
+//   lane (c, h) = (lane % 16, lane / 16);
+//   B column c = output row c of the block: lane (c, h) holds chunk h of the group (32 inputs; the MFMA pair takes
+//     its two 16-input halves);
+//   A row c = (token 4 tg + (c >> 2), limb c & 3): lane (c, h) holds that limb of the inputs of chunk h (limb 3 is
+//     zero);
+//   D: lane (c, h) holds row c x token 4 tg + h, its three limb sums in D[0..2] and, through the C operand (meta), the
+//     bias -OFF * sum(d_j) and the token's activation scale in D[3] -- everything a lane needs stays in the lane.
+//
+// Loads: an item is 16 rows x one quad (512 inputs).  W4: one 16-byte chunk per group (16 rows x 64 B per instruction,
+// the four instructions of an item complete each row's two lines back to back).  W2 and the W3 two-bit planes: one
+// 16-byte chunk pair per lane covers two groups (chunks 2 (h >> 1), 2 (h >> 1) + 1 of group 2 j + (h & 1)); one
+// v_permlane16_swap per dword pair (odd 16-lane rows of the first operand <-> even rows of the second) turns it into
+// the operands of groups 2 j and 2 j + 1.  The W3 third-bit plane the same with 8-byte pairs.
+//
+// Activations: converted once per workgroup into LDS in the A-operand order (per group, half, token group and chunk:
+// the 12 limb rows of 4 tokens, 16 bytes each, 192 bytes; the 12 active lanes of each 16-lane pass hit 12 distinct
+// 16-byte bank slots and the 4 zero-limb lanes read zeros placed at the 4 remaining slots).
+//
+// Work decomposition as the one-token kernel: one persistent workgroup per CU owns a contiguous range of 16-row
+// blocks of one segment; tasks are (block, stripe set), SPLIT per block from a launch-time cost model; a wave keeps
+// the accumulators of its task per (token, group slot), adds a stripe's four slots in order in the lane, and partials
+// of split blocks meet in LDS where the last task adds them in stripe order.
+#include "agens_kernels.h"
+#include "wq_common.h"
+#include "wq_i8_common.h"
+
+// phase timestamps for profiling builds (a build that defines them records them; product builds compile nothing)
+#ifndef AK_M1_STAMP
+#define AK_M1_STAMP(i)
+#endif
+
+namespace agq {
+
+int num_cus();
+
+namespace {
+
+constexpr int kG = 128;
+constexpr int kRsrcWord3 = 0x00020000;  // raw buffer resource, dword 3 (CDNA)
+constexpr int kNt = 2;                    // streaming (non-temporal) cache policy for the weights
+
+// one item of one lane: the raw weight words of the quad's four groups (W2 / W3: before the lane exchange) and the
+// scales of its row for the four groups
+template <int BITS>
+struct QuadRaw;
+template <>
+struct QuadRaw<4> { uint4 w[4]; uint2 s; };
+template <>
+struct QuadRaw<3> { uint4 lo[2]; uint2 hi[2]; uint2 s; };
+template <>
+struct QuadRaw<2> { uint4 lo[2]; uint2 s; };
+
+__device__ __forceinline__ uint2 swap16(uint32_t a, uint32_t b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(a, b, false, false);
+  return make_uint2(r[0], r[1]);
+}
+
+// the raw operand of group s of the quad (after the lane exchange of its pair)
+template <int BITS>
+__device__ __forceinline__ void quad_groups(const QuadRaw<BITS>& q, Raw<BITS> (&r)[4]) {
+  if constexpr (BITS == 4) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) r[s].w = q.w[s];
+  } else {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint2 a = swap16(q.lo[j].x, q.lo[j].z), b = swap16(q.lo[j].y, q.lo[j].w);
+      r[2 * j].lo = make_uint2(a.x, b.x);
+      r[2 * j + 1].lo = make_uint2(a.y, b.y);
+      if constexpr (BITS == 3) {
+        const uint2 hh = swap16(q.hi[j].x, q.hi[j].y);
+        r[2 * j].hi = hh.x;
+        r[2 * j + 1].hi = hh.y;
+      }
+    }
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ T pick4(int i, T v0, T v1, T v2, T v3) {
+  return i == 0 ? v0 : i == 1 ? v1 : i == 2 ? v2 : v3;
+}
+#define AK_PICK(i, arr) pick4((i), (arr)[0], (arr)[1], (arr)[2], (arr)[3])
+static_assert(kMaxSegs == 4, "segment selects cover four segments");
+
+// LDS bytes of the activation image (per group: 2 halves x NT token groups x 4 chunks x 192 B) and its meta
+__host__ __device__ inline int mt_a_bytes(int ngroups, int nt) { return ngroups * 2 * nt * 768; }
+__host__ __device__ inline int mt_meta_bytes(int ngroups, int nt) { return nt * ngroups * 4 * 16; }
+
+template <int BITS, int SPLIT, int DEPTH, int NT>
+__global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
+  extern __shared__ __attribute__((aligned(256))) uint8_t lds[];
+  constexpr int LPU = kG / 8, UPW = 64 / LPU, XB = 4, MP = 4 * NT;  // MP: padded tokens
+  constexpr int REC = 128 * BITS;
+  const int P = a.P, nquad = a.nquad, k = a.k, mm = a.m;
+  const int ngroups = nquad * 4;
+  const int nwv = blockDim.x >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 15, h = lane >> 4;
+  const Segs& sgs = a.segs;
+
+  // this workgroup's segment and its 16-row blocks [b_lo, b_lo + nb) of that segment
+  int sg = 0;
+#pragma unroll
+  for (int i = 1; i < kMaxSegs; ++i) sg += (i < sgs.nseg && (int)blockIdx.x >= a.wg_end[i - 1]) ? 1 : 0;
+  const int wg0 = sg ? AK_PICK(sg - 1, a.wg_end) : 0, gs = AK_PICK(sg, a.wg_end) - wg0, w = blockIdx.x - wg0;
+  const int n = AK_PICK(sg, sgs.n), n_b16 = (n + 15) >> 4;
+  const int b_lo = (int)((long long)w * n_b16 / gs);
+  const int nb = (int)((long long)(w + 1) * n_b16 / gs) - b_lo;
+  uint16_t* const yseg = AK_PICK(sg, sgs.y);
+  const int ldy = AK_PICK(sg, sgs.ldy);
+
+  // LDS: zeros [256 B] | A image [group][half][token group][chunk][4 tokens x 3 limbs x 16 B] |
+  //      meta [token group][group][4 tokens] int4 | outputs [nb][MP][16] bf16 | partials [nb][P][MP][16] | tickets
+  uint8_t* const ximg = lds + 256;
+  const int abytes = mt_a_bytes(ngroups, NT);
+  i32x4* const meta = reinterpret_cast<i32x4*>(ximg + abytes);
+  uint16_t* const yl = reinterpret_cast<uint16_t*>(ximg + abytes + mt_meta_bytes(ngroups, NT));
+  float* const part = reinterpret_cast<float*>(yl + nb * MP * 16);
+  int* const tickets = reinterpret_cast<int*>(part + (SPLIT > 1 ? nb * P * MP * 16 : 0));
+
+  if (SPLIT > 1)
+    for (int i = tid; i < nb; i += 64 * nwv) tickets[i] = 0;
+  if (tid < 64) reinterpret_cast<uint32_t*>(lds)[tid] = 0u;
+
+  // ---- activations, step 1: this lane's bf16 inputs (unit u = (token u / ngroups, group u % ngroups)), requested
+  // and waited for before any weight request
+  const int sub = lane % LPU, units = ngroups * mm, ustride = nwv * UPW;  // real tokens only (padding rows unused)
+  const int u0 = wave * UPW + lane / LPU;
+  const int npass = (units + ustride - 1) / ustride;
+  uint4 xv[XB];
+  auto xload = [&](int pass0) {
+#pragma unroll
+    for (int b = 0; b < XB; ++b) {
+      const int u = u0 + (pass0 + b) * ustride, t = u / ngroups, kk = (u - t * ngroups) * kG + 8 * sub;
+      const bool ok = u < units && t < mm && kk < k;
+      xv[b] = make_uint4(0u, 0u, 0u, 0u);
+      if (pass0 + b < npass) {
+        const uint4 v = *reinterpret_cast<const uint4*>(a.x + (ok ? (size_t)t * k + kk : 0));
+        xv[b] = ok ? v : make_uint4(0u, 0u, 0u, 0u);
+      }
+    }
+  };
+  AK_M1_STAMP(0);
+  xload(0);
+#pragma unroll
+  for (int b = 0; b < XB; ++b) asm volatile("" ::"v"(xv[b].x), "v"(xv[b].y), "v"(xv[b].z), "v"(xv[b].w));
+  AK_M1_STAMP(1);
+
+  // ---- this wave's tasks: stripe set j, quads [qa, qb), blocks b0w, b0w + bstep, ... < nb
+  const int j = wave % SPLIT, bstep = nwv / SPLIT, b0w = wave / SPLIT;
+  const int pa = j * P / SPLIT, pb = (j + 1) * P / SPLIT;
+  const int qa = stripe_begin(pa, nquad, P, 2), qb = stripe_begin(pb, nquad, P, 2);
+  const int ntw = b0w < nb ? (nb - b0w + bstep - 1) / bstep : 0;
+  const int nitems = ntw * (qb - qa);
+  // bit q - qa set when quad q is the last of its stripe (quads < qa + 128)
+  unsigned long long ends0 = 0, ends1 = 0;
+  for (int p = pa; p < pb; ++p) {
+    const int r = stripe_begin(p + 1, nquad, P, 2) - 1 - qa;
+    if (r < 64) ends0 |= 1ull << r;
+    else ends1 |= 1ull << (r - 64);
+  }
+
+  // ---- weight addressing: per lane fixed, per item scalar.  Rows past the segment's end (padding of the last block)
+  // read other rows or, past the buffer, zeros; their results are not written.
+  const int ntile = nquad >> 1;
+  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<void*>(AK_PICK(sg, sgs.wt)), (short)0, ntile * n * REC, kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(AK_PICK(sg, sgs.st)), (short)0, ntile * n * 16, kRsrcWord3);
+  // W2 / W3: the chunk pair 2 (h >> 1), 2 (h >> 1) + 1 of group 2 jj + (h & 1) (jj = 0, 1: 64 B of the row each)
+  const int cp = 4 * (h & 1) + 2 * (h >> 1);
+  const int vo_w = c * REC + (BITS == 4 ? h * 16 : cp * 8), vo_h = c * REC + 256 + cp * 4, vo_s = c * 16;
+  const int tile_w = n * REC, tile_s = n * 16;
+  auto fetch1 = [&](int blk, int qd, QuadRaw<BITS>& d) {
+    const int row0 = (b_lo + blk) * 16, odd = qd & 1;
+    const int so = row0 * REC + (qd >> 1) * tile_w;
+    if constexpr (BITS == 4) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rw, vo_w, so + odd * 256 + s * 64, kNt);
+        d.w[s] = make_uint4(v[0], v[1], v[2], v[3]);
+      }
+    } else {
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rw, vo_w, so + odd * 128 + jj * 64, kNt);
+        d.lo[jj] = make_uint4(v[0], v[1], v[2], v[3]);
+        if constexpr (BITS == 3) {
+          typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+          const u32x2 g2 = __builtin_amdgcn_raw_buffer_load_b64(rw, vo_h, so + odd * 64 + jj * 32, kNt);
+          d.hi[jj] = make_uint2(g2[0], g2[1]);
+        }
+      }
+    }
+    typedef unsigned int u32x2s __attribute__((ext_vector_type(2)));
+    const u32x2s sv = __builtin_amdgcn_raw_buffer_load_b64(rs, vo_s, row0 * 16 + (qd >> 1) * tile_s + odd * 8, 0);
+    d.s = make_uint2(sv[0], sv[1]);
+  };
+
+  QuadRaw<BITS> buf[DEPTH];
+  // fetch cursor (an item past the end reloads quad qa of block 0: cache-resident, never used)
+  int fb = b0w, fq = qa;
+  auto fetch_next = [&](QuadRaw<BITS>& dst) {
+    const bool in = fb < nb;
+    fetch1(in ? fb : 0, in ? fq : qa, dst);
+    const bool wrap = fq + 1 == qb;
+    fq = wrap ? qa : fq + 1;
+    fb = wrap ? fb + bstep : fb;
+  };
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d) fetch_next(buf[d]);
+
+  // ---- activations, step 2: limbs into the A image, bias sums and activation scale into meta
+  auto convert = [&](int p0) {
+#pragma unroll
+    for (int b = 0; b < XB; ++b) {
+      if (p0 + b >= npass || wave * UPW + (p0 + b) * ustride >= units) break;  // no unit of this wave (uniform)
+      const int u = u0 + (p0 + b) * ustride;
+      uint32_t t0[8], t1[8], t2[8];
+      const int e = group_limbs<LPU>(xv[b], t0, t1, t2);
+      const int b0 = dpp_group_reduce<LPU, false>(limb_sum8(t0, 0));
+      const int b1 = dpp_group_reduce<LPU, false>(limb_sum8(t1, 1));
+      const int b2 = dpp_group_reduce<LPU, false>(limb_sum8(t2, 2));
+      if (u < units) {
+        const int t = u / ngroups, g = u - t * ngroups, tg = t >> 2, ui = t & 3;
+        const int eg0 = 8 * sub, ch = eg0 >> 5;
+        store_limbs<BITS>(ximg + ((g * 2) * NT + tg) * 768 + ch * 192 + ui * 48, NT * 768, eg0 & 31, t0, t1, t2);
+        if (sub == 0) {
+          constexpr int OFF = code_offset<BITS>();
+          const i32x4 mv = {-OFF * b0, -OFF * b1, -OFF * b2, act_scale_bits(e)};
+          meta[(tg * ngroups + g) * 4 + ui] = mv;
+        }
+      }
+    }
+  };
+  convert(0);
+  for (int p0 = XB; p0 < npass; p0 += XB) {
+    xload(p0);
+    convert(p0);
+  }
+  __syncthreads();
+  AK_M1_STAMP(2);
+
+  // A role: token (c >> 2) of the token group, limb c & 3 (limb 3 reads zeros at the pass's 4 free bank slots)
+  const bool a_on = (c & 3) < 3;
+  const int a_lane = a_on ? 256 + h * 192 + 16 * (3 * (c >> 2) + (c & 3)) : 16 * ((12 * h + 12 + (c >> 2)) & 15);
+  const int a_gmul = a_on ? 2 * NT * 768 : 0, a_hmul = a_on ? NT * 768 : 0, a_tmul = a_on ? 768 : 0;
+
+  auto write_y = [&](int bl, int tg, float y) {  // row c of local block bl, token 4 tg + h
+    yl[(bl * MP + 4 * tg + h) * 16 + c] = f2bf(y);
+  };
+
+  int cb = b0w, cq = qa, cpp = pa;
+  float acc[NT][4], yrun[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    yrun[t] = 0.f;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) acc[t][s] = 0.f;
+  }
+  // one item without branches: an[][] = the accumulators before a stripe end reset them
+  auto core = [&](const QuadRaw<BITS>& bf, float (&an)[NT][4], bool& end, int& eg, int& ep) {
+    const int r0 = cq - qa;
+    end = ((r0 < 64 ? ends0 >> r0 : ends1 >> (r0 - 64)) & 1ull) != 0;
+    // scales first: the loaded dwords die here (scales live to the end of the item would be copied at the loop latch)
+    float sc[4];
+    sc[0] = __uint_as_float(bf.s.x << 16);
+    sc[1] = __uint_as_float(bf.s.x & 0xFFFF0000u);
+    sc[2] = __uint_as_float(bf.s.y << 16);
+    sc[3] = __uint_as_float(bf.s.y & 0xFFFF0000u);
+    asm volatile("" ::"v"(sc[0]), "v"(sc[1]), "v"(sc[2]), "v"(sc[3]));
+    Raw<BITS> rq[4];
+    quad_groups<BITS>(bf, rq);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      i32x4 b0, b1;
+      make_b<BITS>(rq[s], b0, b1);
+      const int g = 4 * cq + s;
+#pragma unroll
+      for (int tg = 0; tg < NT; ++tg) {
+        const i32x4 mt = meta[(tg * ngroups + g) * 4 + h];
+        const uint8_t* src = lds + a_lane + g * a_gmul + tg * a_tmul;
+        const i32x4 a0 = *reinterpret_cast<const i32x4*>(src);
+        const i32x4 a1 = *reinterpret_cast<const i32x4*>(src + a_hmul);
+        i32x4 d = mt;
+        d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, d, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, d, 0, 0, 0);
+        acc[tg][s] = fmaf(group_sum_f32(d), sc[s] * __int_as_float(mt[3]), acc[tg][s]);
+      }
+    }
+#pragma unroll
+    for (int tg = 0; tg < NT; ++tg)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        an[tg][s] = acc[tg][s];
+        acc[tg][s] = end ? 0.f : acc[tg][s];
+      }
+    eg = cb;
+    ep = cpp;
+    cpp = end ? cpp + 1 : cpp;
+    const bool wrap = cq + 1 == qb;
+    cq = wrap ? qa : cq + 1;
+    cb = wrap ? cb + bstep : cb;
+    cpp = wrap ? pa : cpp;
+  };
+  // a stripe ended: its partial per (row, token) = ((slot 0 + slot 1) + slot 2) + slot 3 in the lane
+  auto stripe_end = [&](const float (&v)[NT][4], int eg, int ep) {
+    float pp[NT];
+#pragma unroll
+    for (int tg = 0; tg < NT; ++tg) pp[tg] = ((v[tg][0] + v[tg][1]) + v[tg][2]) + v[tg][3];
+    if constexpr (SPLIT == 1) {
+#pragma unroll
+      for (int tg = 0; tg < NT; ++tg) {
+        yrun[tg] = ep == 0 ? pp[tg] : yrun[tg] + pp[tg];
+        if (ep == P - 1) write_y(eg, tg, yrun[tg]);
+      }
+    } else {
+#pragma unroll
+      for (int tg = 0; tg < NT; ++tg) part[((eg * P + ep) * MP + 4 * tg + h) * 16 + c] = pp[tg];
+      if (ep + 1 < pb) return;  // more stripes in this task
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");  // LDS only: no wait for loads in flight
+      int last = 0;
+      if (lane == 0) last = atomicAdd(&tickets[eg], 1) == SPLIT - 1;
+      last = __shfl(last, 0);
+      if (last) {
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+        const float* slot = part + eg * P * MP * 16;
+#pragma unroll
+        for (int tg = 0; tg < NT; ++tg) {
+          const int o = (4 * tg + h) * 16 + c;
+          float y = slot[o];
+          for (int q = 1; q < P; ++q) y += slot[q * MP * 16 + o];
+          write_y(eg, tg, y);
+        }
+      }
+    }
+  };
+
+  const int nfull = nitems / DEPTH * DEPTH;
+  for (int i0 = 0; i0 < nfull; i0 += DEPTH) {
+    float sv[DEPTH][NT][4];
+    bool end[DEPTH];
+    int eg[DEPTH], ep[DEPTH];
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      core(buf[d], sv[d], end[d], eg[d], ep[d]);
+      fetch_next(buf[d]);
+    }
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d)
+      if (end[d]) stripe_end(sv[d], eg[d], ep[d]);
+  }
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d) {
+    if (nfull + d < nitems) {
+      float v[NT][4];
+      bool e;
+      int g, p;
+      core(buf[d], v, e, g, p);
+      if (e) stripe_end(v, g, p);
+    }
+  }
+  AK_M1_STAMP(3);
+  __syncthreads();
+  for (int i = tid; i < nb * MP * 16; i += 64 * nwv) {
+    const int bl = i / (MP * 16), t = (i / 16) % MP, row = (b_lo + bl) * 16 + (i & 15);
+    if (t < mm && row < n) yseg[(size_t)t * ldy + row] = yl[i];
+  }
+}
+
+size_t mt_block_bytes(int P, int split, int nt) {  // per 16-row block: outputs, partials, ticket
+  return (size_t)4 * nt * 16 * 2 + (split > 1 ? (size_t)P * 4 * nt * 16 * 4 + 4 : 0);
+}
+
+template <int BITS, int SPLIT, int NT>
+void launch_mt_split(const I8Args& a, int grid, size_t smem, hipStream_t s) {
+  constexpr int DEPTH = 2;
+  hipLaunchKernelGGL((i8_mt_kernel<BITS, SPLIT, DEPTH, NT>), dim3(grid), dim3(1024), smem, s, a);
+}
+
+template <int BITS, int NT>
+int launch_mt(I8Args a, hipStream_t s) {
+  const Segs& g = a.segs;
+  const int ngroups = a.nquad * 4, ntile = a.nquad / 2;
+  const size_t x_bytes = 256 + (size_t)mt_a_bytes(ngroups, NT) + mt_meta_bytes(ngroups, NT);
+  for (int i = 0; i < g.nseg; ++i)  // buffer offsets are 32-bit
+    if ((long long)ntile * g.n[i] * 128 * BITS >= (1ll << 31)) return AK_INVALID;
+  if (x_bytes > 140 * 1024) return AK_INVALID;
+  // workgroups per segment: about the same number of 16-row blocks each, at most one workgroup per CU
+  int total = 0;
+  for (int i = 0; i < g.nseg; ++i) total += (g.n[i] + 15) / 16;
+  const int cus = num_cus();
+  int per = (total + cus - 1) / cus, grid = 0;
+  for (;; ++per) {
+    grid = 0;
+    for (int i = 0; i < g.nseg; ++i) grid += ((g.n[i] + 15) / 16 + per - 1) / per;
+    if (grid <= cus || per >= total) break;
+  }
+  for (int i = 0, e = 0; i < kMaxSegs; ++i) {
+    if (i < g.nseg) e += ((g.n[i] + 15) / 16 + per - 1) / per;
+    a.wg_end[i] = e;
+  }
+  int nbmax = 0;
+  for (int i = 0; i < g.nseg; ++i) {
+    const int nbs = (g.n[i] + 15) / 16, gs = (nbs + per - 1) / per;
+    nbmax = (nbs + gs - 1) / gs > nbmax ? (nbs + gs - 1) / gs : nbmax;
+  }
+  // tasks per block: fewest quad rounds for the busiest wave, a task's overhead counted as about one quad
+  int best_split = 1;
+  double best = 1e30;
+  for (int split : {1, 2, 4, 8}) {
+    if (split > a.P) break;
+    if (x_bytes + (size_t)nbmax * mt_block_bytes(a.P, split, NT) + 16 > 160 * 1024) continue;
+    int lmax = 0;
+    for (int j = 0; j < split; ++j) {
+      const int l = stripe_begin((j + 1) * a.P / split, a.nquad, a.P, 2) - stripe_begin(j * a.P / split, a.nquad, a.P, 2);
+      lmax = l > lmax ? l : lmax;
+    }
+    const int bstep = 16 / split;
+    const double cost = (double)((nbmax + bstep - 1) / bstep) * (lmax + 1.0);
+    if (cost < best - 1e-9) best = cost, best_split = split;
+  }
+  if (best > 1e29) return AK_INVALID;
+  const size_t smem = x_bytes + (size_t)nbmax * mt_block_bytes(a.P, best_split, NT) + 16;
+  switch (best_split) {
+    case 1: launch_mt_split<BITS, 1, NT>(a, grid, smem, s); break;
+    case 2: launch_mt_split<BITS, 2, NT>(a, grid, smem, s); break;
+    case 4: launch_mt_split<BITS, 4, NT>(a, grid, smem, s); break;
+    default: launch_mt_split<BITS, 8, NT>(a, grid, smem, s); break;
+  }
+  return (int)hipGetLastError();
+}
+
+}  // namespace
+
+// 2..8 tokens (4 or 8 in the kernel; the dispatcher sends 3..8), 16-row blocks (the last one padded).  Returns AK_INVALID if the shape does not
+// suit the kernel (group 64, the tokens' activations beyond the LDS, a segment beyond 2 GB): the caller falls back.
+int i8_gemv_mt(int bits, const void* x, int m, const Segs& g, int k, int group, hipStream_t s) {
+  if (group != kG || m < 2 || m > 8) return AK_INVALID;
+  I8Args a;
+  a.segs = g;
+  a.x = static_cast<const uint16_t*>(x);
+  a.m = m;
+  a.k = k;
+  a.nquad = kpad(k) / kG / 4;
+  a.qpt = 2;
+  a.P = stripe_count(a.nquad, a.qpt);
+  a.nb = 0;
+  const int nt = m <= 4 ? 1 : 2;
+  switch (bits * 10 + nt) {
+    case 41: return launch_mt<4, 1>(a, s);
+    case 31: return launch_mt<3, 1>(a, s);
+    case 21: return launch_mt<2, 1>(a, s);
+    case 42: return launch_mt<4, 2>(a, s);
+    case 32: return launch_mt<3, 2>(a, s);
+    case 22: return launch_mt<2, 2>(a, s);
+    default: return AK_INVALID;
+  }
+}
+
+}  // namespace agq
