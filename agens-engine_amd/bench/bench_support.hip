@@ -158,6 +158,68 @@ int agb_run(const AgbLaunch* plan, int nlaunch, int warmup, int steps, int use_g
   return e;
 }
 
+// The plan as one chain (ak_wq_chain_*: every step waits for the one before it, as in a decode step where each linear
+// reads the previous one's output): `warmup` untimed runs, then `steps` runs between two events (one graph launch
+// each with use_graph).  *chained = 1 if the chain ran as one chained launch; *status = ak_wq_chain_status().
+int agb_run_chain(const AgbLaunch* plan, int nlaunch, int warmup, int steps, int use_graph, float* ms, int* chained,
+                  int* status) {
+  std::vector<ak_wq_step> st((size_t)nlaunch);
+  for (int i = 0; i < nlaunch; ++i) {
+    const AgbLaunch& L = plan[i];
+    ak_wq_step& d = st[(size_t)i];
+    memset(&d, 0, sizeof(d));
+    d.bits = L.bits, d.m = L.m, d.nseg = L.nseg, d.k = L.k, d.group = L.group, d.bf16w = L.bf16w, d.x = L.x;
+    for (int j = 0; j < L.nseg; ++j) {
+      d.wt[j] = L.wt[j], d.st[j] = L.st[j], d.y[j] = L.y[j], d.n[j] = L.n[j];
+      d.ldy[j] = L.use_ldy ? L.ldy[j] : 0;
+    }
+  }
+  void* ch = nullptr;
+  int e = ak_wq_chain_create(st.data(), nlaunch, &ch);
+  if (e) return e;
+  *chained = ak_wq_chain_chained(ch);
+  hipStream_t s;
+  e = (int)hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+  if (e) {
+    ak_wq_chain_destroy(ch);
+    return e;
+  }
+  hipEvent_t a, b;
+  hipEventCreate(&a);
+  hipEventCreate(&b);
+  hipGraphExec_t ge = nullptr;
+  hipGraph_t g = nullptr;
+  for (int w = 0; w < (warmup > 0 ? warmup : 1) && !e; ++w) e = ak_wq_chain_run(ch, s);
+  if (!e) e = (int)hipStreamSynchronize(s);
+  if (!e && use_graph) {
+    e = (int)hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+    if (!e) e = ak_wq_chain_run(ch, s);
+    const int e2 = (int)hipStreamEndCapture(s, &g);
+    if (!e) e = e2;
+    if (!e) e = (int)hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+    if (!e) e = (int)hipGraphLaunch(ge, s);
+    if (!e) e = (int)hipStreamSynchronize(s);
+  }
+  if (!e) {
+    hipEventRecord(a, s);
+    for (int r = 0; r < steps && !e; ++r) e = use_graph ? (int)hipGraphLaunch(ge, s) : ak_wq_chain_run(ch, s);
+    hipEventRecord(b, s);
+    if (!e) e = (int)hipEventSynchronize(b);
+    float t = 0.f;
+    if (!e) e = (int)hipEventElapsedTime(&t, a, b);
+    *ms = steps > 0 ? t / steps : 0.f;
+  }
+  *status = ak_wq_chain_status();
+  if (ge) hipGraphExecDestroy(ge);
+  if (g) hipGraphDestroy(g);
+  hipEventDestroy(a);
+  hipEventDestroy(b);
+  hipStreamSynchronize(s);
+  hipStreamDestroy(s);
+  ak_wq_chain_destroy(ch);
+  return e;
+}
+
 // Duration of every launch of the plan (average over `reps` passes), each bracketed by its own pair of events on the
 // launching stream; ms_each[i] in milliseconds.
 int agb_time_each(const AgbLaunch* plan, int nlaunch, int reps, float* ms_each) {

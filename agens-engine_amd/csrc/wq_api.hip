@@ -7,6 +7,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <new>
+
 #include "agens_kernels.h"
 #include "wq_common.h"
 
@@ -17,6 +19,10 @@ int exact_ct_gemv(const void* x, const int32_t* packed, const void* scales, void
 int i8_gemv(int bits, const void* x, int m, const Segs& g, int k, int group, hipStream_t s);
 int i8_gemv_m1(int bits, const void* x, int m, const Segs& g, int k, int group, hipStream_t s);
 int i8_gemv_mt(int bits, const void* x, int m, const Segs& g, int k, int group, hipStream_t s);
+int m1d_chain_make(int nsteps, const int* bits, const void* const* x, const int* m, const int* k, const Segs* segs,
+                   const int* wait, void** table, int* mt_out, size_t* smem_out);
+int m1d_chain_launch(const void* table, int nsteps, int mt, size_t smem, hipStream_t s);
+int m1d_chain_error(int* err);
 
 namespace {
 
@@ -94,6 +100,29 @@ int gemv(int bits, const void* x, int m, int nseg, const void* const* wt, const 
     if (e) return e;
   }
   return 0;
+}
+
+// A chain of GEMV steps: the device step table of the chained kernel, or (table == nullptr) the steps themselves, run
+// one launch each.
+struct Chain {
+  int nsteps = 0, mt = 1;
+  size_t smem = 0;
+  void* table = nullptr;
+  ak_wq_step* steps = nullptr;
+};
+
+int step_args_ok(const ak_wq_step& st) {
+  if (!group_ok(st.k, st.group) || st.nseg < 1 || st.nseg > kMaxSegs || st.m < 1 || st.m > 128) return 0;
+  if (st.bits < 2 || st.bits > 4 || !st.x) return 0;
+  for (int i = 0; i < st.nseg; ++i)
+    if (st.n[i] < 1 || !st.wt[i] || !st.st[i] || !st.y[i] || (st.ldy[i] && st.ldy[i] < st.n[i])) return 0;
+  return 1;
+}
+
+int run_step(const ak_wq_step& st, hipStream_t s) {
+  int ldy[kMaxSegs];
+  for (int i = 0; i < st.nseg; ++i) ldy[i] = st.ldy[i] ? st.ldy[i] : st.n[i];
+  return gemv(st.bits, st.x, st.m, st.nseg, st.wt, st.st, st.y, st.n, ldy, st.k, st.group, st.bf16w, false, s);
 }
 
 }  // namespace
@@ -180,6 +209,78 @@ int ak_w4g128_gemv_bf16_variant(int variant, const void* x, const int32_t* packe
 int ak_w4g128_gemv_bf16(const void* x, const int32_t* packed, const void* scales, void* y, int n, int k,
                         void* stream) {
   return ak_w4g128_gemv_bf16_variant(22, x, packed, scales, y, n, k, stream);
+}
+
+int ak_wq_chain_create(const ak_wq_step* steps, int nsteps, void** chain) {
+  if (!steps || nsteps < 1 || !chain) return AK_INVALID;
+  for (int i = 0; i < nsteps; ++i)
+    if (!step_args_ok(steps[i])) return AK_INVALID;
+  Chain* c = new (std::nothrow) Chain;
+  if (!c) return AK_OOM;
+  c->nsteps = nsteps;
+  c->steps = static_cast<ak_wq_step*>(malloc(sizeof(ak_wq_step) * (size_t)nsteps));
+  if (!c->steps) {
+    delete c;
+    return AK_OOM;
+  }
+  memcpy(c->steps, steps, sizeof(ak_wq_step) * (size_t)nsteps);
+  bool chainable = !exact_mode();
+  for (int i = 0; i < nsteps && chainable; ++i)
+    chainable = steps[i].bf16w == 0 && steps[i].group == 128 && steps[i].m <= 2;
+  if (chainable) {
+    int* ib = static_cast<int*>(malloc(sizeof(int) * 4 * (size_t)nsteps));
+    const void** xs = static_cast<const void**>(malloc(sizeof(void*) * (size_t)nsteps));
+    Segs* sg = static_cast<Segs*>(malloc(sizeof(Segs) * (size_t)nsteps));
+    int e = ib && xs && sg ? 0 : AK_OOM;
+    if (!e) {
+      int *bits = ib, *m = ib + nsteps, *k = ib + 2 * nsteps, *wait = ib + 3 * nsteps;
+      for (int i = 0; i < nsteps; ++i) {
+        const ak_wq_step& st = steps[i];
+        int ldy[kMaxSegs];
+        for (int j = 0; j < st.nseg; ++j) ldy[j] = st.ldy[j] ? st.ldy[j] : st.n[j];
+        bits[i] = st.bits, m[i] = st.m, k[i] = st.k, wait[i] = !st.independent, xs[i] = st.x;
+        sg[i] = make_segs(st.nseg, st.wt, st.st, st.y, st.n, ldy, 16);
+      }
+      e = m1d_chain_make(nsteps, bits, xs, m, k, sg, wait, &c->table, &c->mt, &c->smem);
+    }
+    free(ib);
+    free(xs);
+    free(sg);
+    if (e && e != AK_INVALID) {  // AK_INVALID: a step does not suit the chained kernel (one launch per step)
+      free(c->steps);
+      delete c;
+      return e;
+    }
+  }
+  *chain = c;
+  return 0;
+}
+
+int ak_wq_chain_run(void* chain, void* stream) {
+  if (!chain) return AK_INVALID;
+  const Chain* c = static_cast<const Chain*>(chain);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (c->table) return m1d_chain_launch(c->table, c->nsteps, c->mt, c->smem, s);
+  for (int i = 0; i < c->nsteps; ++i)
+    if (const int e = run_step(c->steps[i], s)) return e;
+  return 0;
+}
+
+int ak_wq_chain_chained(void* chain) { return chain && static_cast<const Chain*>(chain)->table ? 1 : 0; }
+
+int ak_wq_chain_destroy(void* chain) {
+  if (!chain) return 0;
+  Chain* c = static_cast<Chain*>(chain);
+  const int e = c->table ? (int)hipFree(c->table) : 0;
+  free(c->steps);
+  delete c;
+  return e;
+}
+
+int ak_wq_chain_status(void) {
+  int err = 0;
+  const int e = m1d_chain_error(&err);
+  return e ? -e : err;
 }
 
 int ak_w4_set_mma(int mode) {

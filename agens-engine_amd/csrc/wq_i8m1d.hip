@@ -33,6 +33,8 @@
 // the load offsets are a fixed per-lane part plus a scalar part of (block, tile), the cursors advance by selects,
 // and a stripe that ends inside the group only leaves a copy of its accumulators; the group's epilogue turns those
 // into stripe partials.
+#include <stdlib.h>
+
 #include "agens_kernels.h"
 #include "wq_common.h"
 #include "wq_i8_common.h"
@@ -60,6 +62,8 @@ namespace {
 constexpr int kG = 128, kCPQ = 16;
 constexpr int kRsrcWord3 = 0x00020000;  // raw buffer resource, dword 3 (CDNA)
 constexpr int kNt = 2;                    // streaming (non-temporal) cache policy for the weights
+constexpr int kVmcnt0 = 0x0F70;            // s_waitcnt immediate: vector memory counter 0, the others unconstrained
+constexpr int kSc1 = 16;                  // device-scope coherent access (sc1): misses / writes through the L2
 
 // one tile item of one lane: the raw weight words of both quads (before the W2 / W3 lane exchange) and the dwords
 // holding the two quads' scales
@@ -106,21 +110,81 @@ __device__ __forceinline__ T pick4(int i, T v0, T v1, T v2, T v3) {
 #define AK_PICK(i, arr) pick4((i), (arr)[0], (arr)[1], (arr)[2], (arr)[3])
 static_assert(kMaxSegs == 4, "segment selects cover four segments");
 
-template <int BITS, int SPLIT, int DEPTH, int MT>
-__global__ void __launch_bounds__(1024, 1) i8_m1d_kernel(const I8Args a) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  AK_M1_WG_BEGIN();
+// Chained launches (several GEMV steps in one persistent launch): a workgroup signals the end of a step by writing
+// its flag word (one per workgroup, 64 bytes apart) with the step count, after its outputs are stored with
+// device-coherent (sc1, L2 write-through) stores and acknowledged; a step that reads earlier steps' outputs first
+// issues its first weight loads (constant data), then waits until every workgroup's flag has reached the step, then
+// reads its activations with device-coherent loads.  No L2 write-back or invalidate is needed on either side.
+constexpr int kChainMaxWg = 1024, kChainFlagStride = 16;
+constexpr long long kChainSpinTicks = 20000000;  // 0.2 s of the 100 MHz wall clock: a bounded wait, then an error
+__device__ uint32_t g_chain_flags[kChainMaxWg * kChainFlagStride];
+__device__ uint32_t g_chain_err;
+
+// per-step phase timestamps of a chained launch, in probe builds only (-DAK_CHAIN_PROBE; product builds compile
+// nothing): [step][workgroup][phase] = wall clock (100 MHz) when thread 0 passed: 0 step start, 1 activations
+// requested after the wait, 2 activations converted, 3 item loop done (all waves), 4 step signalled
+#ifdef AK_CHAIN_PROBE
+constexpr int kProbeSteps = 320;
+__device__ unsigned long long g_probe[kProbeSteps * kChainMaxWg * 8];
+#define AK_PROBE(s, i)                                                                  \
+  do {                                                                                   \
+    if (threadIdx.x == 0 && (s) < kProbeSteps)                                           \
+      g_probe[((size_t)(s) * kChainMaxWg + blockIdx.x) * 8 + (i)] = wall_clock64();      \
+  } while (0)
+#else
+#define AK_PROBE(s, i)
+#endif
+
+// Wave 0 polls until the flags of workgroups [0, nwg) are all at least `target` (wrap-safe).  It polls before it
+// requests weights of its own, so that no poll waits behind them.
+__device__ __forceinline__ void chain_poll(uint32_t target) {
+  const int lane = threadIdx.x, nwg = gridDim.x;
+  const long long t0 = wall_clock64();
+  for (;;) {
+    bool ok = true;
+    for (int j = lane; j < nwg; j += 64) {
+      const uint32_t v = __hip_atomic_load(g_chain_flags + j * kChainFlagStride, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+      ok = ok && (int)(v - target) >= 0;
+    }
+    if (__all(ok)) break;
+    if (wall_clock64() - t0 > kChainSpinTicks) {
+      if (lane == 0) __hip_atomic_store(&g_chain_err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+// the workgroup meets at an LDS-only barrier (the weight loads in flight stay in flight)
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// One GEMV step of one workgroup.  CHAIN: part of a chained launch (workgroups past the step's grid return at once;
+// with `wait`, the step waits for all workgroups to reach `target` after its first weight requests; activations are
+// read and outputs written device-coherently).
+template <int BITS, int SPLIT, int DEPTH, int MT, bool CHAIN>
+__device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wait, uint32_t target, int ps = 0) {
+  AK_PROBE(ps, 0);
   constexpr int LPU = kG / 8, UPW = 64 / LPU, XB = 4;
   constexpr int REC = 128 * BITS;  // one row's tile record
   const int P = a.P, nquad = a.nquad, k = a.k, mm = a.m;  // mm <= MT tokens (the others are zero, not written)
   const int ntile = nquad >> 1;
   const int nwv = blockDim.x >> 6;
-  const int tid = threadIdx.x, lane = tid & 63;
+  int tid = threadIdx.x;
+  // chained: an opaque thread index per step, so that nothing lane-dependent is hoisted out of the step loop (the
+  // hoisted values would stay live across every step's item loop)
+  if constexpr (CHAIN) asm volatile("" : "+v"(tid));
+  const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 15, h = lane >> 4;
   const int rr = c >> 2, vv = c & 3;  // B role: row of the block, group of the quad
   const Segs& sgs = a.segs;
 
+  if (CHAIN && (int)blockIdx.x >= AK_PICK(sgs.nseg - 1, a.wg_end)) return;  // no rows of this step
   // this workgroup's segment and its blocks [b_lo, b_lo + nb) of that segment
   int sg = 0;
 #pragma unroll
@@ -154,6 +218,9 @@ __global__ void __launch_bounds__(1024, 1) i8_m1d_kernel(const I8Args a) {
   const int u0 = wave * UPW + lane / LPU;
   const int npass = (units + ustride - 1) / ustride;
   uint4 xv[XB];
+  const __amdgpu_buffer_rsrc_t rx =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.x), (short)0, mm * k * 2, kRsrcWord3);
+  (void)rx;
   auto xload = [&](int pass0) {
 #pragma unroll
     for (int b = 0; b < XB; ++b) {
@@ -162,15 +229,24 @@ __global__ void __launch_bounds__(1024, 1) i8_m1d_kernel(const I8Args a) {
       const bool ok = u < units && t < mm && kk < k;
       xv[b] = make_uint4(0u, 0u, 0u, 0u);
       if (pass0 + b < npass) {
-        const uint4 v = *reinterpret_cast<const uint4*>(a.x + (ok ? (size_t)t * k + kk : 0));
-        xv[b] = ok ? v : make_uint4(0u, 0u, 0u, 0u);
+        if constexpr (CHAIN) {  // device-coherent: x may be an earlier step's output, written by another XCD
+          const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? (int)(((size_t)t * k + kk) * 2) : 0, 0, kSc1);
+          xv[b] = ok ? make_uint4(v[0], v[1], v[2], v[3]) : make_uint4(0u, 0u, 0u, 0u);
+        } else {
+          const uint4 v = *reinterpret_cast<const uint4*>(a.x + (ok ? (size_t)t * k + kk : 0));
+          xv[b] = ok ? v : make_uint4(0u, 0u, 0u, 0u);
+        }
       }
     }
   };
+  // a chained step that depends on earlier steps requests its first weights before it waits for them (below)
+  const bool late_x = CHAIN && wait;
   AK_M1_STAMP(0);
-  xload(0);
+  if (!late_x) {
+    xload(0);
 #pragma unroll
-  for (int b = 0; b < XB; ++b) asm volatile("" ::"v"(xv[b].x), "v"(xv[b].y), "v"(xv[b].z), "v"(xv[b].w));
+    for (int b = 0; b < XB; ++b) asm volatile("" ::"v"(xv[b].x), "v"(xv[b].y), "v"(xv[b].z), "v"(xv[b].w));
+  }
   AK_M1_STAMP(1);
 
   // ---- this wave's tasks: stripe set j, tiles [ta, tb), blocks b0w, b0w + bstep, ... < nb
@@ -237,8 +313,14 @@ __global__ void __launch_bounds__(1024, 1) i8_m1d_kernel(const I8Args a) {
 
   // ---- the first DEPTH items are requested, then step 2 of the activations: per group the limbs (to LDS), and in
   // meta the bias sums -OFF * sum(d_j) of the three limbs with the activation scale 2^(E - 148) as float bits
+  if (late_x && wave == 0) chain_poll(target);
 #pragma unroll
   for (int d = 0; d < DEPTH; ++d) fetch_next(buf[d]);
+  if (late_x) {
+    lds_barrier();
+    xload(0);
+  }
+  AK_PROBE(ps, 1);
 
   auto convert = [&](int p0) {
 #pragma unroll
@@ -269,6 +351,7 @@ __global__ void __launch_bounds__(1024, 1) i8_m1d_kernel(const I8Args a) {
   }
   __syncthreads();
   AK_M1_STAMP(2);
+  AK_PROBE(ps, 2);
 
   // A role: group c >> 2, limb c & 3 (limb 3 reads zeros), chunk 4 * (c >> 2) + h of the quad; half 1 is kCPQ * 48
   // bytes further
@@ -400,10 +483,23 @@ __global__ void __launch_bounds__(1024, 1) i8_m1d_kernel(const I8Args a) {
   }
   AK_M1_STAMP(3);
   __syncthreads();
+  AK_PROBE(ps, 3);
   for (int i = tid; i < MT * nb * 4; i += 64 * nwv) {
     const int t = MT == 1 ? 0 : i / (nb * 4), row = b_lo * 4 + i - t * nb * 4;
-    if (t < mm && row < n) yseg[(size_t)t * ldy + row] = yl[i];
+    if (t < mm && row < n) {
+      if constexpr (CHAIN)
+        __hip_atomic_store(yseg + (size_t)t * ldy + row, yl[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      else
+        yseg[(size_t)t * ldy + row] = yl[i];
+    }
   }
+}
+
+template <int BITS, int SPLIT, int DEPTH, int MT>
+__global__ void __launch_bounds__(1024, 1) i8_m1d_kernel(const I8Args a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  AK_M1_WG_BEGIN();
+  m1d_body<BITS, SPLIT, DEPTH, MT, false>(a, lds, false, 0u);
   AK_M1_WG_END();
 }
 
@@ -412,21 +508,21 @@ size_t m1d_block_bytes(int P, int split, int mt) {  // per 4-row block: outputs,
   return (size_t)mt * 8 + (split > 1 ? (size_t)P * 16 * mt + 4 : 0);
 }
 
-template <int BITS, int SPLIT, int MT>
-void launch_split(const I8Args& a, int grid, int nwv, size_t smem, hipStream_t s) {
-  constexpr int DEPTH = MT <= 2 ? AK_M1_TILES : 1;  // items in flight per wave
-  hipLaunchKernelGGL((i8_m1d_kernel<BITS, SPLIT, DEPTH, MT>), dim3(grid), dim3(64 * nwv), smem, s, a);
-}
+// Launch shape of one GEMV step: workgroups per segment (about the same number of 4-row blocks each, at most one
+// workgroup per CU), waves per workgroup and stripe sets per block (SPLIT).  chain: 16 waves (a chained launch has one
+// block size).  Returns AK_INVALID if the shape does not suit the kernel.
+struct M1dShape {
+  int split, nwv, grid;
+  size_t smem;
+};
 
-template <int BITS, int MT>
-int launch_m1d(I8Args a, hipStream_t s) {
+int plan_m1d(I8Args& a, int bits, int mt, bool chain, M1dShape& sh) {
   const Segs& g = a.segs;
-  const size_t x_bytes = m1d_x_bytes(a.nquad, MT);
+  const size_t x_bytes = m1d_x_bytes(a.nquad, mt);
   const int ntile = a.nquad / 2;
   for (int i = 0; i < g.nseg; ++i)  // buffer offsets are 32-bit
-    if ((long long)ntile * g.n[i] * 128 * BITS >= (1ll << 31)) return AK_INVALID;
+    if ((long long)ntile * g.n[i] * 128 * bits >= (1ll << 31)) return AK_INVALID;
   if (x_bytes > 150 * 1024) return AK_INVALID;
-  // workgroups per segment: about the same number of blocks each, at most one workgroup per CU
   int total = 0;
   for (int i = 0; i < g.nseg; ++i) total += (g.n[i] + 3) / 4;
   const int cus = num_cus();
@@ -449,10 +545,11 @@ int launch_m1d(I8Args a, hipStream_t s) {
   // about half an item; ties go to more waves (latency hiding) and fewer waves per block (less exchange)
   int best_split = 1, best_nwv = 16;
   double best = 1e30;
-  for (int nwv : {16, 8})
+  for (int nwv : {16, 8}) {
+    if (chain && nwv != 16) continue;
     for (int split : {1, 2, 4, 8}) {
       if (split > a.P) break;
-      if (x_bytes + (size_t)nbmax * m1d_block_bytes(a.P, split, MT) + 16 > 160 * 1024) continue;
+      if (x_bytes + (size_t)nbmax * m1d_block_bytes(a.P, split, mt) + 16 > 160 * 1024) continue;
       int lmax = 0;
       for (int j = 0; j < split; ++j) {
         const int l = (stripe_begin((j + 1) * a.P / split, a.nquad, a.P, 2) -
@@ -463,15 +560,74 @@ int launch_m1d(I8Args a, hipStream_t s) {
       const double cost = (double)((nbmax + bstep - 1) / bstep) * (lmax + 0.5);
       if (cost < best - 1e-9) best = cost, best_split = split, best_nwv = nwv;
     }
+  }
   if (best > 1e29) return AK_INVALID;
-  const size_t smem = x_bytes + (size_t)nbmax * m1d_block_bytes(a.P, best_split, MT) + 16;
-  switch (best_split) {
-    case 1: launch_split<BITS, 1, MT>(a, grid, best_nwv, smem, s); break;
-    case 2: launch_split<BITS, 2, MT>(a, grid, best_nwv, smem, s); break;
-    case 4: launch_split<BITS, 4, MT>(a, grid, best_nwv, smem, s); break;
-    default: launch_split<BITS, 8, MT>(a, grid, best_nwv, smem, s); break;
+  sh.split = best_split;
+  sh.nwv = best_nwv;
+  sh.grid = grid;
+  sh.smem = x_bytes + (size_t)nbmax * m1d_block_bytes(a.P, best_split, mt) + 16;
+  return 0;
+}
+
+constexpr int m1d_depth(int mt) { return mt <= 2 ? AK_M1_TILES : 1; }  // items in flight per wave
+
+template <int BITS, int SPLIT, int MT>
+void launch_split(const I8Args& a, int grid, int nwv, size_t smem, hipStream_t s) {
+  hipLaunchKernelGGL((i8_m1d_kernel<BITS, SPLIT, m1d_depth(MT), MT>), dim3(grid), dim3(64 * nwv), smem, s, a);
+}
+
+template <int BITS, int MT>
+int launch_m1d(I8Args a, hipStream_t s) {
+  M1dShape sh;
+  if (plan_m1d(a, BITS, MT, false, sh)) return AK_INVALID;
+  switch (sh.split) {
+    case 1: launch_split<BITS, 1, MT>(a, sh.grid, sh.nwv, sh.smem, s); break;
+    case 2: launch_split<BITS, 2, MT>(a, sh.grid, sh.nwv, sh.smem, s); break;
+    case 4: launch_split<BITS, 4, MT>(a, sh.grid, sh.nwv, sh.smem, s); break;
+    default: launch_split<BITS, 8, MT>(a, sh.grid, sh.nwv, sh.smem, s); break;
   }
   return (int)hipGetLastError();
+}
+
+// ---- chained launches: one persistent workgroup per CU runs the steps in order
+struct ChainStep {
+  I8Args a;
+  int kind;  // bits * 16 + SPLIT
+  int wait;  // 1: the step reads (or overwrites) what earlier steps wrote or read: wait for all of them
+};
+
+template <int MT>
+__global__ void __launch_bounds__(1024, 1) i8_chain_kernel(const ChainStep* __restrict__ steps, int nsteps) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  constexpr int D = m1d_depth(MT);
+  uint32_t* const flag = g_chain_flags + blockIdx.x * kChainFlagStride;
+  // every workgroup's flag holds the same count between chained launches (all of them signal every step)
+  const uint32_t f0 = __builtin_amdgcn_readfirstlane(__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  for (int s = 0; s < nsteps; ++s) {
+    const ChainStep st = steps[s];  // a copy: the step's fields live in scalar registers
+    const bool w = st.wait != 0;
+    const uint32_t target = f0 + (uint32_t)s;
+    switch (st.kind) {
+      case 4 * 16 + 1: m1d_body<4, 1, D, MT, true>(st.a, lds, w, target, s); break;
+      case 4 * 16 + 2: m1d_body<4, 2, D, MT, true>(st.a, lds, w, target, s); break;
+      case 4 * 16 + 4: m1d_body<4, 4, D, MT, true>(st.a, lds, w, target, s); break;
+      case 4 * 16 + 8: m1d_body<4, 8, D, MT, true>(st.a, lds, w, target, s); break;
+      case 3 * 16 + 1: m1d_body<3, 1, D, MT, true>(st.a, lds, w, target, s); break;
+      case 3 * 16 + 2: m1d_body<3, 2, D, MT, true>(st.a, lds, w, target, s); break;
+      case 3 * 16 + 4: m1d_body<3, 4, D, MT, true>(st.a, lds, w, target, s); break;
+      case 3 * 16 + 8: m1d_body<3, 8, D, MT, true>(st.a, lds, w, target, s); break;
+      case 2 * 16 + 1: m1d_body<2, 1, D, MT, true>(st.a, lds, w, target, s); break;
+      case 2 * 16 + 2: m1d_body<2, 2, D, MT, true>(st.a, lds, w, target, s); break;
+      case 2 * 16 + 4: m1d_body<2, 4, D, MT, true>(st.a, lds, w, target, s); break;
+      default: m1d_body<2, 8, D, MT, true>(st.a, lds, w, target, s); break;
+    }
+    // signal: this workgroup's outputs of steps <= s are stored (each wave waits for its own stores' acknowledgement,
+    // which for sc1 stores means written through to device scope)
+    __builtin_amdgcn_s_waitcnt(kVmcnt0);
+    __syncthreads();
+    if (threadIdx.x == 0) __hip_atomic_store(flag, f0 + (uint32_t)s + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    AK_PROBE(s, 4);
+  }
 }
 
 }  // namespace
@@ -506,6 +662,79 @@ int i8_gemv_m1(int bits, const void* x, int m, const Segs& g, int k, int group, 
     case 28: return launch_m1d<2, 8>(a, s);
     default: return AK_INVALID;
   }
+}
+
+// ---- chained launches (host side)
+
+// Table of a chain's steps in device memory, or AK_INVALID if some step does not suit the chained kernel (group 64,
+// more than two tokens, activations beyond the LDS, a segment beyond 2 GB): the caller then runs the steps one launch
+// each.  x[i], m[i], k[i], bits[i], segs[i], wait[i] describe step i.
+int m1d_chain_make(int nsteps, const int* bits, const void* const* x, const int* m, const int* k, const Segs* segs,
+                   const int* wait, void** table, int* mt_out, size_t* smem_out) {
+  int mt = 1;
+  for (int i = 0; i < nsteps; ++i) {
+    if (m[i] < 1 || m[i] > 2 || bits[i] < 2 || bits[i] > 4) return AK_INVALID;
+    mt = m[i] > mt ? m[i] : mt;
+  }
+  if (num_cus() > kChainMaxWg) return AK_INVALID;
+  ChainStep* h = static_cast<ChainStep*>(calloc((size_t)nsteps, sizeof(ChainStep)));
+  if (!h) return AK_OOM;
+  size_t smem = 0;
+  for (int i = 0; i < nsteps; ++i) {
+    I8Args& a = h[i].a;
+    a.segs = segs[i];
+    a.x = static_cast<const uint16_t*>(x[i]);
+    a.m = m[i];
+    a.k = k[i];
+    a.nquad = kpad(k[i]) / kG / 4;
+    a.qpt = 2;
+    a.P = stripe_count(a.nquad, a.qpt);
+    a.nb = 0;
+    M1dShape sh;
+    if (plan_m1d(a, bits[i], mt, true, sh)) {
+      free(h);
+      return AK_INVALID;
+    }
+    h[i].kind = bits[i] * 16 + sh.split;
+    h[i].wait = i > 0 && wait[i] ? 1 : 0;
+    smem = sh.smem > smem ? sh.smem : smem;
+  }
+  void* d = nullptr;
+  int e = (int)hipMalloc(&d, (size_t)nsteps * sizeof(ChainStep));
+  if (!e) e = (int)hipMemcpy(d, h, (size_t)nsteps * sizeof(ChainStep), hipMemcpyHostToDevice);
+  free(h);
+  if (e) {
+    if (d) hipFree(d);
+    return e == (int)hipErrorOutOfMemory ? AK_OOM : e;
+  }
+  *table = d;
+  *mt_out = mt;
+  *smem_out = smem;
+  return 0;
+}
+
+int m1d_chain_launch(const void* table, int nsteps, int mt, size_t smem, hipStream_t s) {
+  const ChainStep* t = static_cast<const ChainStep*>(table);
+  if (mt == 1)
+    hipLaunchKernelGGL(i8_chain_kernel<1>, dim3(num_cus()), dim3(1024), smem, s, t, nsteps);
+  else
+    hipLaunchKernelGGL(i8_chain_kernel<2>, dim3(num_cus()), dim3(1024), smem, s, t, nsteps);
+  return (int)hipGetLastError();
+}
+
+#ifdef AK_CHAIN_PROBE
+extern "C" int ak_chain_probe_read(void* dst, size_t bytes) {
+  return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_probe), bytes, 0, hipMemcpyDeviceToHost);
+}
+#endif
+
+// reads and clears the flag a chained launch raises when a wait ran out (0.2 s): 1 if one did since the last call
+int m1d_chain_error(int* err) {
+  uint32_t v = 0, z = 0;
+  int e = (int)hipMemcpyFromSymbol(&v, HIP_SYMBOL(g_chain_err), sizeof(v), 0, hipMemcpyDeviceToHost);
+  if (!e && v) e = (int)hipMemcpyToSymbol(HIP_SYMBOL(g_chain_err), &z, sizeof(z), 0, hipMemcpyHostToDevice);
+  *err = (int)v;
+  return e;
 }
 
 }  // namespace agq

@@ -57,6 +57,8 @@ def load_libs():
         ("agb_gen_x", i, [ctypes.c_uint64, sz, ctypes.c_float, vp, vp]),
         ("agb_run", i, [ctypes.POINTER(AgbLaunch), i, i, i, i, ctypes.POINTER(ctypes.c_float)]),
         ("agb_time_each", i, [ctypes.POINTER(AgbLaunch), i, i, ctypes.POINTER(ctypes.c_float)]),
+        ("agb_run_chain", i, [ctypes.POINTER(AgbLaunch), i, i, i, i, ctypes.POINTER(ctypes.c_float),
+                              ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int)]),
         ("agb_read_bw", i, [sz, i, ctypes.POINTER(ctypes.c_float)]),
     ]:
         f = getattr(B, name)
@@ -249,9 +251,20 @@ def run_sweep(args, K, B):
     plan, meta, cpu = build_sweep(ctx, args.m, cpu_layers)
     print(f"# sweep generated in {time.time() - t0:.1f} s ({len(plan)} launches)", file=sys.stderr, flush=True)
     arr = (AgbLaunch * len(plan))(*plan)
-    ms = ctypes.c_float()
-    ctx.check(B.agb_run(arr, len(plan), args.warmup, args.steps, 0 if args.eager else 1, ctypes.byref(ms)), "run")
     total_bytes = sum(algo_bytes(L) for L in plan)
+    # one launch per linear (the reference's launch pattern without programmatic launch edges)
+    ms_l = ctypes.c_float()
+    ctx.check(B.agb_run(arr, len(plan), args.warmup, args.steps, 0 if args.eager else 1, ctypes.byref(ms_l)), "run")
+    # the sweep as one chain (ak_wq_chain_run): the headline unless --no-chain
+    ms_c, chained, status = ctypes.c_float(), ctypes.c_int(0), ctypes.c_int(0)
+    use_chain = not args.no_chain
+    if use_chain:
+        ctx.check(B.agb_run_chain(arr, len(plan), args.warmup, args.steps, 0 if args.eager else 1, ctypes.byref(ms_c),
+                                  ctypes.byref(chained), ctypes.byref(status)), "chain run")
+        if status.value != 0:
+            raise RuntimeError(f"chained sweep: ak_wq_chain_status() = {status.value} (a bounded wait ran out)")
+        use_chain = chained.value == 1
+    ms = ms_c if use_chain else ms_l
     gbs = total_bytes / (ms.value * 1e-3) / 1e9
     # per launch class (linear, bit width; one kernel instance per shape): its launches of the sweep replayed alone
     # as one graph, back to back like in the sweep; the class with the most time is the dominant kernel
@@ -279,6 +292,21 @@ def run_sweep(args, K, B):
             traffic = json.load(open(tf)).get(dom_name, {}).get("bytes_per_launch")
         except (OSError, ValueError):
             traffic = None
+    if use_chain:  # the dominant (only) kernel is the chained launch: one dispatch per sweep
+        ctraffic = None
+        if args.m == 1 and os.path.exists(tf):
+            try:
+                ctraffic = json.load(open(tf)).get("chain_sweep", {}).get("bytes_per_launch")
+            except (OSError, ValueError):
+                ctraffic = None
+        roof = {"bound": "hbm", "kernel": "i8_chain_kernel (whole sweep, one dispatch)", "achieved": round(gbs, 1),
+                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": ctraffic,
+                "launches": 1, "avg_us": round(ms.value * 1e3, 1), "bytes_per_launch": total_bytes}
+    else:
+        roof = {"bound": "hbm", "kernel": f"i8_m1d_kernel ({dom_name})", "achieved": round(achieved, 1),
+                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                "launches": dom["launches"], "avg_us": round(dom["ms"] * 1e3 / dom["launches"], 2),
+                "bytes_per_launch": dom["bytes"] // dom["launches"]}
     out = {
         "metric": "effective HBM GB/s (% of peak) + us per 64-layer 32B decode GEMV sweep, M=1",
         "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -290,11 +318,16 @@ def run_sweep(args, K, B):
                                "gate_up 5120->55296, down 27648->5120, mixed W2/W3/W4 g128 per layer, "
                                "+ W4 LM head 5120->152064",
                    "m": args.m, "layers_by_bits": bits_mix, "launches": len(plan),
-                   "bytes_per_sweep": total_bytes, "graph": not args.eager, "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "kernel": f"i8_m1d_kernel ({dom_name})", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "launches": dom["launches"], "avg_us": round(dom["ms"] * 1e3 / dom["launches"], 2),
-                     "bytes_per_launch": dom["bytes"] // dom["launches"]},
+                   "bytes_per_sweep": total_bytes, "graph": not args.eager, "parallelism": "single GPU",
+                   "chained": use_chain},
+        "roofline": roof,
+        "one_launch_per_linear": {"us_per_sweep": round(ms_l.value * 1e3, 1),
+                                  "GBps": round(total_bytes / (ms_l.value * 1e-3) / 1e9, 1),
+                                  "dominant_class": {"kernel": f"i8_m1d_kernel ({dom_name})",
+                                                     "GBps": round(achieved, 1), "launches": dom["launches"],
+                                                     "avg_us": round(dom["ms"] * 1e3 / dom["launches"], 2),
+                                                     "bytes_per_launch": dom["bytes"] // dom["launches"],
+                                                     "traffic": traffic}},
         "stream_read_ceiling_GBps": round(read_bw.value, 1),
         "per_linear": detail,
         "cpu_baseline": cpu_res,
@@ -345,6 +378,7 @@ def main():
     ap.add_argument("--config", default="sweep")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true")
+    ap.add_argument("--no-chain", action="store_true", help="time the sweep as one launch per linear only")
     ap.add_argument("--exact", action="store_true", help="the reference's exact fp32 numerics instead")
     ap.add_argument("--calib", action="store_true",
                     help="first copy 256 MiB with a plain copy kernel (the known-size reference for HBM counters)")

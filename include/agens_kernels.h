@@ -110,6 +110,41 @@ int ak_w4_dequant_kt_rows(const void* wt, const void* st, void* w, int n, int k,
 int ak_w3_dequant_kt_rows(const void* wt, const void* st, void* w, int n, int k, int group, int r0, int nr,
                           void* stream);          /* agens_kernels.h:247-248 */
 
+/* ---------------------------------------------------------------------------------------------- chained GEMV steps
+ * No single counterpart in the reference: it replaces a run of ak_wq_gemv_kt_multi launches joined by programmatic
+ * dependent launch edges in a captured graph (reference: ak_graph_pdl, kernels/src/runtime.cu:198-230, and the
+ * kernel-side contract of kernels/include/agens_pdl.cuh:1-16: a GEMV may read its constant weights before the kernel
+ * it depends on has finished, and reads x / writes y only after).  MI355X has no programmatic launch edges between
+ * same-stream kernels, so the steps run in ONE persistent launch: each step issues its first weight loads, waits for
+ * every workgroup to finish the previous step (a grid barrier over per-workgroup flag words in device memory), then
+ * reads its activations.  Results are bit-identical to running the steps one ak_wq_gemv_kt_multi call each, in order.
+ *
+ * A step has ak_wq_gemv_kt_multi's arguments (ldy[i] = 0: n[i]).  independent = 1 declares that the step reads and
+ * writes nothing that the steps since the last dependent step write (or read, for its writes): it then does not wait.
+ * The chained kernel takes steps of group 128 with m <= 2 on the default numerics; any other chain runs as one
+ * ak_wq_gemv_kt_multi call per step (same results, no overlap).
+ *   ak_wq_chain_create  validates the steps (as ak_wq_gemv_kt_multi: 1 on a bad argument), allocates and uploads the
+ *                       chain's step table (device memory, synchronous); not under stream capture;
+ *   ak_wq_chain_run     one launch on `stream`, allocates nothing, capturable; at most one chained launch may run on
+ *                       a device at a time (they share the device's flag words);
+ *   ak_wq_chain_status  after the stream is synchronized: 1 if a chained launch's bounded wait (0.2 s) ran out since
+ *                       the last call (its outputs are then not valid), else 0; negative: a HIP error. */
+typedef struct ak_wq_step {
+  int bits, m, nseg, k, group, bf16w;
+  const void* x;
+  const void* wt[4];
+  const void* st[4];
+  void* y[4];
+  int n[4];
+  int ldy[4];
+  int independent;
+} ak_wq_step;
+int ak_wq_chain_create(const ak_wq_step* steps, int nsteps, void** chain);
+int ak_wq_chain_run(void* chain, void* stream);
+int ak_wq_chain_chained(void* chain); /* 1: runs as one chained launch, 0: one launch per step */
+int ak_wq_chain_destroy(void* chain);
+int ak_wq_chain_status(void);
+
 /* ---------------------------------------------------------------------------------------------- switches
  * reference: agens_kernels.h:205 / :208 / :211, w4_gemv.cu:3271-3282.  mma: -1 auto (environment AGENS_W4_EXACT), 0 exact
  * fp32 path, 1 default integer-MFMA path.  lean / tma select bit-identical sm90-only variants in the reference;

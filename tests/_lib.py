@@ -192,6 +192,56 @@ def header_symbols():
     return sorted(set(re.findall(r"\b(ak_\w+)\s*\(", txt)))
 
 
+class WqStep(ctypes.Structure):
+    """ak_wq_step of include/agens_kernels.h (one GEMV step of a chain)."""
+    _fields_ = [("bits", c_int), ("m", c_int), ("nseg", c_int), ("k", c_int), ("group", c_int), ("bf16w", c_int),
+                ("x", c_void_p), ("wt", c_void_p * 4), ("st", c_void_p * 4), ("y", c_void_p * 4), ("n", c_int * 4),
+                ("ldy", c_int * 4), ("independent", c_int)]
+
+
+def _addr(v):
+    if isinstance(v, Dev):
+        return v.p.value
+    return v.value if isinstance(v, c_void_p) else v
+
+
+def wq_step(bits, x, m, lins, ys, k, group=128, ldy=None, independent=0, bf16w=0):
+    """A chain step over the Linear segments `lins` with outputs `ys` (Dev or addresses), x a Dev or an address."""
+    st = WqStep()
+    st.bits, st.m, st.nseg, st.k, st.group, st.bf16w = bits, m, len(lins), k, group, bf16w
+    st.x = _addr(x)
+    for i, (L, y) in enumerate(zip(lins, ys)):
+        st.wt[i], st.st[i], st.y[i], st.n[i] = L.wt.p.value, L.st.p.value, _addr(y), L.n
+        st.ldy[i] = ldy[i] if ldy else 0
+    st.independent = independent
+    return st
+
+
+class Chain:
+    """ak_wq_chain_create / _run / _destroy over a list of WqStep."""
+
+    def __init__(self, steps):
+        K = kernels()
+        self.steps = (WqStep * len(steps))(*steps)
+        self.h = c_void_p()
+        check(K.ak_wq_chain_create(self.steps, len(steps), ctypes.byref(self.h)), "ak_wq_chain_create")
+
+    @property
+    def chained(self):
+        return kernels().ak_wq_chain_chained(self.h) == 1
+
+    def run(self):
+        check(kernels().ak_wq_chain_run(self.h, None), "ak_wq_chain_run")
+
+    def __del__(self):
+        try:
+            if self.h:
+                kernels().ak_wq_chain_destroy(self.h)
+                self.h = None
+        except Exception:
+            pass
+
+
 _ker = None
 
 
@@ -243,6 +293,11 @@ def kernels():
             "ak_w4_dequant_kt": (i, [vp, vp, vp, i, i, i, vp]),
             "ak_w4_dequant_kt_rows": (i, [vp, vp, vp, i, i, i, i, i, vp]),
             "ak_w3_dequant_kt_rows": (i, [vp, vp, vp, i, i, i, i, i, vp]),
+            "ak_wq_chain_create": (i, [ctypes.POINTER(WqStep), i, ctypes.POINTER(c_void_p)]),
+            "ak_wq_chain_run": (i, [vp, vp]),
+            "ak_wq_chain_chained": (i, [vp]),
+            "ak_wq_chain_destroy": (i, [vp]),
+            "ak_wq_chain_status": (i, []),
             "ak_w4_set_mma": (i, [i]),
             "ak_w4_set_lean": (i, [i]),
             "ak_w4_set_tma": (i, [i]),

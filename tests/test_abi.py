@@ -62,3 +62,24 @@ def test_switches(K):
     assert K.ak_w4_set_lean(2) == 0 and K.ak_w4_set_lean(-1) == 0
     assert K.ak_w4_set_tma(4) == 0 and K.ak_w4_set_tma(-1) == 0
     assert K.ak_error_string(1)
+
+
+def test_chain_invalid_arguments_return_1_without_a_gpu(K):
+    from _lib import WqStep
+    h = ctypes.c_void_p()
+    st = (WqStep * 1)()
+    s = st[0]
+    s.bits, s.m, s.nseg, s.k, s.group, s.x = 4, 1, 1, 1024, 128, 1
+    s.wt[0] = s.st[0] = s.y[0] = 1
+    s.n[0] = 16
+    assert K.ak_wq_chain_create(st, 0, ctypes.byref(h)) == 1  # no steps
+    assert K.ak_wq_chain_create(None, 1, ctypes.byref(h)) == 1
+    for field, bad in (("group", 96), ("k", 1000), ("nseg", 5), ("m", 0), ("m", 129), ("bits", 5)):
+        good = getattr(s, field)
+        setattr(s, field, bad)
+        assert K.ak_wq_chain_create(st, 1, ctypes.byref(h)) == 1, field
+        setattr(s, field, good)
+    s.ldy[0] = 8  # ldy below n
+    assert K.ak_wq_chain_create(st, 1, ctypes.byref(h)) == 1
+    assert K.ak_wq_chain_run(None, None) == 1
+    assert K.ak_wq_chain_destroy(None) == 0

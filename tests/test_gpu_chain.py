@@ -1,0 +1,215 @@
+"""Chained GEMV steps (ak_wq_chain_*) on the GPU: one persistent launch that runs a list of ak_wq_gemv_kt_multi steps
+with grid barriers between them (the MI355X counterpart of the reference's programmatic-dependent-launch chains of
+GEMV kernels, kernels/src/runtime.cu:198-230, kernels/include/agens_pdl.cuh:1-16).
+
+Every step here reads what the step before it wrote (decoder-layer data flow: qkv -> o -> gate_up -> down -> next
+layer), so a missing or leaky barrier, or a stale (non-coherent) read of another XCD's output, changes the results.
+Bar: bit-identical to the oracle's default numerics applied step by step, and to one ak_wq_gemv_kt_multi launch per
+step.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+from _lib import (kernels, check, Dev, Linear, gemv, gen_container, gen_scales, gen_x, ora_repack, ora_fast, wq_step,
+                  Chain)
+
+pytestmark = pytest.mark.gpu
+
+# E[q^2] of uniform codes q in [-2^(b-1), 2^(b-1) - 1]: scales |N(0,1)| * sa with sa = 1 / sqrt(k E[q^2]) keep the
+# outputs of a long chain at about unit size
+EQ2 = {4: 21.5, 3: 5.5, 2: 1.5}
+
+
+@pytest.fixture(scope="module", autouse=True)
+def gpu():
+    K = kernels()
+    n = ctypes.c_int(0)
+    assert K.ak_device_count(ctypes.byref(n)) == 0 and n.value >= 1, "no GPU visible"
+    K.ak_w4_set_mma(1)
+    assert K.ak_wq_chain_status() == 0
+    yield K
+    K.ak_w4_set_mma(-1)
+
+
+class Lin:
+    """A linear with its host KT copy (for the oracle)."""
+
+    def __init__(self, seed, n, k, bits, group=128):
+        lo, span = -(1 << (bits - 1)), 1 << bits
+        packed = gen_container(seed, n, k, lo, span)
+        scales = gen_scales(seed + 1, n * k // group, 1.0 / np.sqrt(k * EQ2[bits]), 1e-6)
+        self.L = Linear(packed, scales, n, k, group, bits)
+        check(self.L.rc, "repack")
+        rc, self.wt, self.st = ora_repack(bits, packed, scales, n, k, group)
+        assert rc == 0
+        self.n, self.k, self.bits, self.group = n, k, bits, group
+
+
+def layer_plan(seed, bits, H, KV, INTER, group=128):
+    q, kk, v = Lin(seed, H, H, bits, group), Lin(seed + 2, KV, H, bits, group), Lin(seed + 4, KV, H, bits, group)
+    o, gu, dn = Lin(seed + 6, H, H, bits, group), Lin(seed + 8, 2 * INTER, H, bits, group), \
+        Lin(seed + 10, H, INTER, bits, group)
+    return [q, kk, v], o, gu, dn
+
+
+def build(m, layers, H, KV, INTER, group=128):
+    """Steps of `layers` decoder layers: qkv(x=h) -> o(x=q) -> gate_up(x=o) -> down(x=gate_up[:INTER]) -> h."""
+    h = Dev(m * H * 2)
+    steps, flow = [], []  # flow: (step's linears, x buffer, k, outputs)
+    x = h
+    for li, bits in enumerate(layers):
+        qkv, o, gu, dn = layer_plan(1000 + 37 * li, bits, H, KV, INTER, group)
+        yq, yk, yv = Dev(m * H * 2), Dev(m * KV * 2), Dev(m * KV * 2)
+        yo, ygu, yh = Dev(m * H * 2), Dev(m * 2 * INTER * 2), Dev(m * H * 2)
+        for lins, xin, k, ys in [(qkv, x, H, [yq, yk, yv]), ([o], yq, H, [yo]), ([gu], yo, H, [ygu]),
+                                 ([dn], ygu, INTER, [yh])]:
+            steps.append(wq_step(bits, xin, m, [l.L for l in lins], ys, k, group))
+            flow.append((lins, xin, k, ys))
+        x = yh
+    return h, steps, flow
+
+
+def oracle_flow(h_host, m, flow):
+    """The oracle applied step by step: expected outputs of every step (a dict buffer id -> flat uint16)."""
+    vals = {}
+    first_x = flow[0][1]
+    vals[id(first_x)] = h_host
+    out = []
+    for lins, xin, k, ys in flow:
+        xv = vals[id(xin)][: m * k] if id(xin) in vals else None
+        assert xv is not None and xv.size == m * k
+        res = []
+        for l, y in zip(lins, ys):
+            r = ora_fast(l.bits, xv, m, l.wt, l.st, l.n, k, l.group).reshape(-1)
+            vals[id(y)] = r
+            res.append(r)
+        out.append(res)
+    return out
+
+
+def read_outputs(m, flow):
+    return [[y.get(np.uint16, m * l.n) for l, y in zip(lins, ys)] for lins, _, _, ys in flow]
+
+
+def zero_outputs(flow):
+    for _, _, _, ys in flow:
+        for y in ys:
+            z = np.zeros(y.nbytes, np.uint8)
+            check(kernels().ak_memcpy_h2d(y.p, z.ctypes.data, y.nbytes), "zero")
+
+
+def assert_same(got, want, what):
+    for si, (g, w) in enumerate(zip(got, want)):
+        for j, (a, b) in enumerate(zip(g, w)):
+            if not np.array_equal(a, b):
+                bad = int(np.sum(a != b))
+                raise AssertionError(f"{what}: step {si} segment {j}: {bad} of {a.size} outputs differ")
+
+
+@pytest.mark.parametrize("m", [1, 2])
+def test_chain_data_flow_matches_oracle_and_launches(m):
+    K = kernels()
+    H, KV, INTER = 2048, 256, 2560  # INTER = 2.5 tiles: the padded last tile in down's k
+    h, steps, flow = build(m, [3, 2, 4], H, KV, INTER)
+    ch = Chain(steps)
+    assert ch.chained
+    h_host = gen_x(77 + m, m * H)
+    check(K.ak_memcpy_h2d(h.p, h_host.ctypes.data, h_host.nbytes), "h2d")
+    want = oracle_flow(h_host, m, flow)
+    ch.run()
+    check(K.ak_synchronize(), "sync")
+    assert K.ak_wq_chain_status() == 0
+    assert_same(read_outputs(m, flow), want, "chain vs oracle")
+    # the same steps one launch each
+    zero_outputs(flow)
+    for lins, xin, k, ys in flow:
+        gemv(lins[0].bits, xin.p, m, [l.L for l in lins], k, 128, ys=ys)
+    check(K.ak_synchronize(), "sync")
+    assert_same(read_outputs(m, flow), want, "launches vs oracle")
+
+
+def test_chain_replays_with_new_inputs():
+    """Each replay reads the inputs of its own run: a stale read of an earlier run's values would show."""
+    K = kernels()
+    H, KV, INTER = 1024, 128, 1536
+    h, steps, flow = build(1, [4, 3], H, KV, INTER)
+    ch = Chain(steps)
+    assert ch.chained
+    for rep in range(4):
+        h_host = gen_x(500 + rep, H)
+        check(K.ak_memcpy_h2d(h.p, h_host.ctypes.data, h_host.nbytes), "h2d")
+        ch.run()
+        if rep == 2:  # a plain launch between chained runs (the flag words persist across launches)
+            lins, xin, k, ys = flow[0]
+            gemv(lins[0].bits, xin.p, 1, [l.L for l in lins], k, 128, ys=ys)
+            ch.run()
+        check(K.ak_synchronize(), "sync")
+        assert K.ak_wq_chain_status() == 0
+        assert_same(read_outputs(1, flow), oracle_flow(h_host, 1, flow), f"replay {rep}")
+
+
+def test_chain_independent_steps():
+    """A: x -> y1, B (independent): x -> y2, C: y1 -> y3, D (independent of C): y2 -> y4."""
+    K = kernels()
+    k = 2048
+    a, b = Lin(11, 2048, k, 3), Lin(13, 1024, k, 4)
+    c, d = Lin(15, 512, 2048, 2), Lin(17, 768, 1024, 3)
+    x = Dev(k * 2)
+    y1, y2, y3, y4 = Dev(2048 * 2), Dev(1024 * 2), Dev(512 * 2), Dev(768 * 2)
+    steps = [wq_step(3, x, 1, [a.L], [y1], k), wq_step(4, x, 1, [b.L], [y2], k, independent=1),
+             wq_step(2, y1, 1, [c.L], [y3], 2048), wq_step(3, y2, 1, [d.L], [y4], 1024, independent=1)]
+    ch = Chain(steps)
+    assert ch.chained
+    xh = gen_x(99, k)
+    check(K.ak_memcpy_h2d(x.p, xh.ctypes.data, xh.nbytes), "h2d")
+    ch.run()
+    check(K.ak_synchronize(), "sync")
+    assert K.ak_wq_chain_status() == 0
+    r1 = ora_fast(3, xh, 1, a.wt, a.st, a.n, k, 128).reshape(-1)
+    r2 = ora_fast(4, xh, 1, b.wt, b.st, b.n, k, 128).reshape(-1)
+    r3 = ora_fast(2, r1, 1, c.wt, c.st, c.n, 2048, 128).reshape(-1)
+    r4 = ora_fast(3, r2, 1, d.wt, d.st, d.n, 1024, 128).reshape(-1)
+    for y, r, n, name in [(y1, r1, 2048, "A"), (y2, r2, 1024, "B"), (y3, r3, 512, "C"), (y4, r4, 768, "D")]:
+        assert np.array_equal(y.get(np.uint16, n), r), name
+
+
+def test_chain_fallback_runs_steps_one_launch_each():
+    """A group-64 step (and m > 2) cannot run chained: the chain runs one launch per step, same results."""
+    K = kernels()
+    H, KV, INTER = 1024, 128, 1024
+    for group, m in [(64, 1), (128, 4)]:
+        h, steps, flow = build(m, [4, 2], H, KV, INTER, group)
+        ch = Chain(steps)
+        assert not ch.chained
+        h_host = gen_x(31, m * H)
+        check(K.ak_memcpy_h2d(h.p, h_host.ctypes.data, h_host.nbytes), "h2d")
+        ch.run()
+        check(K.ak_synchronize(), "sync")
+        assert_same(read_outputs(m, flow), oracle_flow(h_host, m, flow), f"fallback group {group} m {m}")
+
+
+def test_chain_at_decode_shapes_matches_launches():
+    """Two 32B-shaped layers (QKV 5120 -> 5120 + 2 x 1024, O, gate_up 5120 -> 55296, down 27648 -> 5120): the chained
+    launch equals one launch per step bit for bit (the oracle is too slow at these sizes to run step by step)."""
+    K = kernels()
+    H, KV, INTER = 5120, 1024, 27648
+    h, steps, flow = build(1, [3, 2], H, KV, INTER)
+    ch = Chain(steps)
+    assert ch.chained
+    h_host = gen_x(4242, H)
+    check(K.ak_memcpy_h2d(h.p, h_host.ctypes.data, h_host.nbytes), "h2d")
+    ch.run()
+    check(K.ak_synchronize(), "sync")
+    assert K.ak_wq_chain_status() == 0
+    got = read_outputs(1, flow)
+    zero_outputs(flow)
+    for lins, xin, k, ys in flow:
+        gemv(lins[0].bits, xin.p, 1, [l.L for l in lins], k, 128, ys=ys)
+    check(K.ak_synchronize(), "sync")
+    assert_same(got, read_outputs(1, flow), "chain vs launches")
+    # outputs stay finite and non-trivial through the chain (the data flow carries information)
+    last = got[-1][0].astype(np.uint32) << 16
+    f = last.view(np.float32)
+    assert np.all(np.isfinite(f)) and np.std(f) > 0.05
