@@ -161,8 +161,16 @@ int agb_run(const AgbLaunch* plan, int nlaunch, int warmup, int steps, int use_g
 // The plan as one chain (ak_wq_chain_*: every step waits for the one before it, as in a decode step where each linear
 // reads the previous one's output): `warmup` untimed runs, then `steps` runs between two events (one graph launch
 // each with use_graph).  *chained = 1 if the chain ran as one chained launch; *status = ak_wq_chain_status().
+int agb_run_chain_ex(const AgbLaunch* plan, int nlaunch, int warmup, int steps, int use_graph, float* ms, int* chained,
+                     int* status, int independent);
 int agb_run_chain(const AgbLaunch* plan, int nlaunch, int warmup, int steps, int use_graph, float* ms, int* chained,
                   int* status) {
+  return agb_run_chain_ex(plan, nlaunch, warmup, steps, use_graph, ms, chained, status, 0);
+}
+// independent = 1: every step declared independent of the others (no grid barriers; the caller gives every step its
+// own outputs): the streaming bound of the chained kernel without the decode data flow
+int agb_run_chain_ex(const AgbLaunch* plan, int nlaunch, int warmup, int steps, int use_graph, float* ms, int* chained,
+                     int* status, int independent) {
   std::vector<ak_wq_step> st((size_t)nlaunch);
   for (int i = 0; i < nlaunch; ++i) {
     const AgbLaunch& L = plan[i];
@@ -173,6 +181,7 @@ int agb_run_chain(const AgbLaunch* plan, int nlaunch, int warmup, int steps, int
       d.wt[j] = L.wt[j], d.st[j] = L.st[j], d.y[j] = L.y[j], d.n[j] = L.n[j];
       d.ldy[j] = L.use_ldy ? L.ldy[j] : 0;
     }
+    d.independent = independent;
   }
   void* ch = nullptr;
   int e = ak_wq_chain_create(st.data(), nlaunch, &ch);

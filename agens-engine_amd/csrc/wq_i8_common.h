@@ -187,5 +187,66 @@ __device__ __forceinline__ void store_limbs(uint8_t* dst, size_t half_stride, in
 
 
 
+// One unit of a group-128 activation image: a group of 128 inputs of one token held by 16 lanes, 8 consecutive inputs
+// each (o0 = the lane's first input within its 32-input lane chunk).  Computes what group_limbs, store_limbs and the
+// limb sums do, with fewer operations:
+//   - the group's largest exponent field is the exponent of the largest magnitude (packed 16-bit maxima of the sign-
+//     cleared patterns; NaN / Inf patterns order above every finite one, as their exponent fields do);
+//   - W4: the limb dwords are gathered with byte permutes and their sums taken from the same dwords (sdot4);
+//   - the limb-0 and limb-1 sums of the group share one packed reduction (|sum| <= 128 * 128 < 2^15).
+// Returns e; d0..d2 = the group's limb sums (every lane of the unit).  store = false: nothing is written.
+template <int BITS>
+__device__ __forceinline__ int convert_unit(const uint4 v, uint8_t* dst, size_t half_stride, int o0, bool store,
+                                            int& d0, int& d1, int& d2) {
+  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+  auto mag = [](uint32_t w) {
+    const uint32_t m = w & 0x7FFF7FFFu;
+    return __builtin_bit_cast(u16x2, m);
+  };
+  const u16x2 mx = __builtin_elementwise_max(__builtin_elementwise_max(mag(v.x), mag(v.y)),
+                                             __builtin_elementwise_max(mag(v.z), mag(v.w)));
+  const int e = dpp_group_reduce<16, true>(max((int)mx.x, (int)mx.y)) >> 7;
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  uint32_t t0[8], t1[8], t2[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t b16 = (w[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
+    const int xi = (int)ldexpf(bf2f(b16), 148 - e);  // exact; truncation toward zero
+    t0[i] = (uint32_t)xi;
+    t1[i] = (uint32_t)xi + 0x80u;
+    t2[i] = (uint32_t)xi + 0x8080u;
+  }
+  int s0 = 0, s1 = 0, s2 = 0;
+  if constexpr (BITS == 4) {
+    // word o0 / 8 of each limb row: even inputs -> half 0, odd -> half 1
+    const int v4 = o0 >> 3;
+#pragma unroll
+    for (int limb = 0; limb < 3; ++limb) {
+      const uint32_t* t = limb == 0 ? t0 : limb == 1 ? t1 : t2;
+      const uint32_t sel = (uint32_t)limb | ((uint32_t)(4 + limb) << 8) | 0x0C0C0000u;  // [a.byte l, b.byte l, 0, 0]
+      int s = 0;
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        const uint32_t lo = __builtin_amdgcn_perm(t[hf + 2], t[hf], sel);
+        const uint32_t hi = __builtin_amdgcn_perm(t[hf + 6], t[hf + 4], sel);
+        const uint32_t d = lo | (hi << 16);
+        s = __builtin_amdgcn_sdot4((int)d, 0x01010101, s, false);
+        if (store) *reinterpret_cast<uint32_t*>(dst + hf * half_stride + limb * 16 + 4 * v4) = d;
+      }
+      (limb == 0 ? s0 : limb == 1 ? s1 : s2) = s;
+    }
+  } else {
+    s0 = limb_sum8(t0, 0);
+    s1 = limb_sum8(t1, 1);
+    s2 = limb_sum8(t2, 2);
+    if (store) store_limbs<BITS>(dst, half_stride, o0, t0, t1, t2);
+  }
+  const int p01 = dpp_group_reduce<16, false>(s0 + (int)((uint32_t)s1 << 16));
+  d2 = dpp_group_reduce<16, false>(s2);
+  d0 = (int)(short)(p01 & 0xFFFF);
+  d1 = (p01 - d0) >> 16;
+  return e;
+}
+
 }  // namespace
 }  // namespace agq

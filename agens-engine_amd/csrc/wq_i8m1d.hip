@@ -131,8 +131,16 @@ __device__ unsigned long long g_probe[kProbeSteps * kChainMaxWg * 8];
     if (threadIdx.x == 0 && (s) < kProbeSteps)                                           \
       g_probe[((size_t)(s) * kChainMaxWg + blockIdx.x) * 8 + (i)] = wall_clock64();      \
   } while (0)
+// per wave (lane 0): 0 item loop entered, 1 first group of items computed, 2 item loop left
+__device__ unsigned long long g_probe_w[kProbeSteps * 256 * 16 * 4];
+#define AK_PROBE_W(s, i)                                                                                 \
+  do {                                                                                                    \
+    if ((threadIdx.x & 63) == 0 && (s) < kProbeSteps && blockIdx.x < 256)                                 \
+      g_probe_w[(((size_t)(s) * 256 + blockIdx.x) * 16 + (threadIdx.x >> 6)) * 4 + (i)] = wall_clock64(); \
+  } while (0)
 #else
 #define AK_PROBE(s, i)
+#define AK_PROBE_W(s, i)
 #endif
 
 // Wave 0 polls until the flags of workgroups [0, nwg) are all at least `target` (wrap-safe).  It polls before it
@@ -327,15 +335,13 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
     for (int b = 0; b < XB; ++b) {
       if (p0 + b >= npass || wave * UPW + (p0 + b) * ustride >= units) break;  // no unit of this wave (uniform)
       const int u = u0 + (p0 + b) * ustride;
-      uint32_t t0[8], t1[8], t2[8];
-      const int e = group_limbs<LPU>(xv[b], t0, t1, t2);
-      const int b0 = dpp_group_reduce<LPU, false>(limb_sum8(t0, 0));
-      const int b1 = dpp_group_reduce<LPU, false>(limb_sum8(t1, 1));
-      const int b2 = dpp_group_reduce<LPU, false>(limb_sum8(t2, 2));
-      if (u < units) {
-        const int t = MT == 1 ? 0 : u / gpt, ut = u - t * gpt;
-        const int qd = ut >> 2, gq = ut & 3, eg0 = 8 * sub, cqd = gq * 4 + (eg0 >> 5);
-        store_limbs<BITS>(xq + t * tstride + qd * kCPQ * 96 + cqd * 48, kCPQ * 48, eg0 & 31, t0, t1, t2);
+      const bool live = u < units;
+      const int t = MT == 1 || !live ? 0 : u / gpt, ut = live ? u - t * gpt : 0;
+      const int qd = ut >> 2, gq = ut & 3, eg0 = 8 * sub, cqd = gq * 4 + (eg0 >> 5);
+      int b0, b1, b2;
+      const int e = convert_unit<BITS>(xv[b], xq + t * tstride + qd * kCPQ * 96 + cqd * 48, kCPQ * 48, eg0 & 31, live,
+                                       b0, b1, b2);
+      if (live) {
         if (sub == 0) {
           constexpr int OFF = code_offset<BITS>();
           const i32x4 mv = {-OFF * b0, -OFF * b1, -OFF * b2, act_scale_bits(e)};
@@ -457,6 +463,7 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
   };
 
   const int nfull = nitems / DEPTH * DEPTH;
+  AK_PROBE_W(ps, 0);
   for (int i0 = 0; i0 < nfull; i0 += DEPTH) {
     float sv[DEPTH][MT];
     bool end[DEPTH];
@@ -469,6 +476,7 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d)
       if (end[d]) stripe_end(sv[d], eg[d], ep[d]);
+    if (i0 == 0) AK_PROBE_W(ps, 1);
   }
   // the last, partial group (its later fetches load the cache-resident dummy item)
 #pragma unroll
@@ -482,6 +490,7 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
     }
   }
   AK_M1_STAMP(3);
+  AK_PROBE_W(ps, 2);
   __syncthreads();
   AK_PROBE(ps, 3);
   for (int i = tid; i < MT * nb * 4; i += 64 * nwv) {
@@ -725,6 +734,9 @@ int m1d_chain_launch(const void* table, int nsteps, int mt, size_t smem, hipStre
 #ifdef AK_CHAIN_PROBE
 extern "C" int ak_chain_probe_read(void* dst, size_t bytes) {
   return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_probe), bytes, 0, hipMemcpyDeviceToHost);
+}
+extern "C" int ak_chain_probe_read_w(void* dst, size_t bytes) {
+  return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_probe_w), bytes, 0, hipMemcpyDeviceToHost);
 }
 #endif
 

@@ -224,15 +224,13 @@ __global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
     for (int b = 0; b < XB; ++b) {
       if (p0 + b >= npass || wave * UPW + (p0 + b) * ustride >= units) break;  // no unit of this wave (uniform)
       const int u = u0 + (p0 + b) * ustride;
-      uint32_t t0[8], t1[8], t2[8];
-      const int e = group_limbs<LPU>(xv[b], t0, t1, t2);
-      const int b0 = dpp_group_reduce<LPU, false>(limb_sum8(t0, 0));
-      const int b1 = dpp_group_reduce<LPU, false>(limb_sum8(t1, 1));
-      const int b2 = dpp_group_reduce<LPU, false>(limb_sum8(t2, 2));
-      if (u < units) {
-        const int t = u / ngroups, g = u - t * ngroups, tg = t >> 2, ui = t & 3;
-        const int eg0 = 8 * sub, ch = eg0 >> 5;
-        store_limbs<BITS>(ximg + ((g * 2) * NT + tg) * 768 + ch * 192 + ui * 48, NT * 768, eg0 & 31, t0, t1, t2);
+      const bool live = u < units;
+      const int t = live ? u / ngroups : 0, g = live ? u - t * ngroups : 0, tg = t >> 2, ui = t & 3;
+      const int eg0 = 8 * sub, ch = eg0 >> 5;
+      int b0, b1, b2;
+      const int e = convert_unit<BITS>(xv[b], ximg + ((g * 2) * NT + tg) * 768 + ch * 192 + ui * 48, NT * 768,
+                                       eg0 & 31, live, b0, b1, b2);
+      if (live) {
         if (sub == 0) {
           constexpr int OFF = code_offset<BITS>();
           const i32x4 mv = {-OFF * b0, -OFF * b1, -OFF * b2, act_scale_bits(e)};
