@@ -59,9 +59,10 @@ Segs make_segs(int nseg, const void* const* wt, const void* const* st, void* con
   return g;
 }
 
-// the default path for m <= 16 tokens, in chunks of at most 8: the tokens-in-A-rows kernel (wq_i8mt.hip) for 3..8
-// tokens and the line-load kernel (wq_i8m1d.hip) for one or two (or where the first does not fit) when the tokens'
-// activations fit the LDS, otherwise the any-m kernel (wq_i8.hip)
+// the default path for m <= 16 tokens, in launches of at most 8: one or two tokens on the line-load kernel
+// (wq_i8m1d.hip) when their activations fit the LDS (measured faster there), otherwise and for 3..8 tokens the
+// tokens-in-A-rows kernel (wq_i8mt.hip; activations beyond the LDS in chunks of stripes), and the any-m kernel
+// (wq_i8.hip) for what neither takes (group 64)
 int run_i8(int bits, const void* x, int m, const Segs& g, int k, int group, hipStream_t s) {
   const int mt = m <= 8 ? m : (m + 1) / 2;
   bool ok = true;
@@ -70,7 +71,8 @@ int run_i8(int bits, const void* x, int m, const Segs& g, int k, int group, hipS
     Segs gg = g;
     for (int i = 0; i < g.nseg; ++i) gg.y[i] = g.y[i] + (size_t)m0 * g.ldy[i];
     const void* xx = static_cast<const uint16_t*>(x) + (size_t)m0 * k;
-    int e = mm >= 3 ? i8_gemv_mt(bits, xx, mm, gg, k, group, s) : AK_INVALID;  // measured: 2 tokens faster below
+    int e = mm <= 2 ? i8_gemv_m1(bits, xx, mm, gg, k, group, s) : AK_INVALID;
+    if (e == AK_INVALID) e = i8_gemv_mt(bits, xx, mm, gg, k, group, s);
     if (e == AK_INVALID) e = i8_gemv_m1(bits, xx, mm, gg, k, group, s);
     if (e == AK_INVALID && m0 == 0) {
       ok = false;

@@ -93,17 +93,20 @@ static_assert(kMaxSegs == 4, "segment selects cover four segments");
 __host__ __device__ inline int mt_a_bytes(int ngroups, int nt) { return ngroups * 2 * nt * 768; }
 __host__ __device__ inline int mt_meta_bytes(int ngroups, int nt) { return nt * ngroups * 4 * 16; }
 
-template <int BITS, int SPLIT, int DEPTH, int NT>
+// CH: the stripes are processed in a.nb chunks one after the other (all waves on one chunk's stripes, each chunk with
+// its own activation image), for activations beyond the LDS; stripe partials wait in the LDS and are added in stripe
+// order at the end, so the results are those of an unchunked launch.
+template <int BITS, int SPLIT, int DEPTH, int NT, bool CH>
 __global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
+  static_assert(!CH || SPLIT == 1, "a chunked launch gives every wave whole stripes of its blocks");
   extern __shared__ __attribute__((aligned(256))) uint8_t lds[];
   constexpr int LPU = kG / 8, UPW = 64 / LPU, XB = 4, MP = 4 * NT;  // MP: padded tokens
   constexpr int REC = 128 * BITS;
   const int P = a.P, nquad = a.nquad, k = a.k, mm = a.m;
   const int ngroups = nquad * 4;
   const int nwv = blockDim.x >> 6;
-  const int tid = threadIdx.x, lane = tid & 63;
+  const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int c = lane & 15, h = lane >> 4;
   const Segs& sgs = a.segs;
 
   // this workgroup's segment and its 16-row blocks [b_lo, b_lo + nb) of that segment
@@ -117,29 +120,53 @@ __global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
   uint16_t* const yseg = AK_PICK(sg, sgs.y);
   const int ldy = AK_PICK(sg, sgs.ldy);
 
+  // chunks of stripes and the groups an activation image holds (the largest chunk's)
+  const int nch = CH ? a.nb : 1;
+  int cgs = ngroups;
+  if constexpr (CH) {
+    cgs = 0;
+    for (int q = 0; q < nch; ++q) {
+      const int gq = 4 * (stripe_begin((q + 1) * P / nch, nquad, P, 2) - stripe_begin(q * P / nch, nquad, P, 2));
+      cgs = gq > cgs ? gq : cgs;
+    }
+  }
+
   // LDS: zeros [256 B] | A image [group][half][token group][chunk][4 tokens x 3 limbs x 16 B] |
   //      meta [token group][group][4 tokens] int4 | outputs [nb][MP][16] bf16 | partials [nb][P][MP][16] | tickets
   uint8_t* const ximg = lds + 256;
-  const int abytes = mt_a_bytes(ngroups, NT);
+  const int abytes = mt_a_bytes(cgs, NT);
   i32x4* const meta = reinterpret_cast<i32x4*>(ximg + abytes);
-  uint16_t* const yl = reinterpret_cast<uint16_t*>(ximg + abytes + mt_meta_bytes(ngroups, NT));
+  uint16_t* const yl = reinterpret_cast<uint16_t*>(ximg + abytes + mt_meta_bytes(cgs, NT));
   float* const part = reinterpret_cast<float*>(yl + nb * MP * 16);
-  int* const tickets = reinterpret_cast<int*>(part + (SPLIT > 1 ? nb * P * MP * 16 : 0));
+  int* const tickets = reinterpret_cast<int*>(part + (SPLIT > 1 || CH ? nb * P * MP * 16 : 0));
 
   if (SPLIT > 1)
     for (int i = tid; i < nb; i += 64 * nwv) tickets[i] = 0;
   if (tid < 64) reinterpret_cast<uint32_t*>(lds)[tid] = 0u;
 
-  // ---- activations, step 1: this lane's bf16 inputs (unit u = (token u / ngroups, group u % ngroups)), requested
-  // and waited for before any weight request
-  const int sub = lane % LPU, units = ngroups * mm, ustride = nwv * UPW;  // real tokens only (padding rows unused)
+  // one chunk (an unchunked launch calls it once, outside any loop: a one-trip loop around the item loop makes the
+  // compiler spill)
+  auto run_chunk = [&](int ch) {
+  // chunked: an opaque thread index per chunk, so that nothing lane-dependent is hoisted out of the chunk loop (the
+  // hoisted values would stay live across every chunk's item loop)
+  int tidc = tid;
+  if constexpr (CH) asm volatile("" : "+v"(tidc));
+  const int lane = tidc & 63, c = lane & 15, h = lane >> 4;
+  // this chunk: stripes [cpa, cpb), groups [g0, g0 + cg) (the whole k unless CH)
+  const int cpa = CH ? ch * P / nch : 0, cpb = CH ? (ch + 1) * P / nch : P;
+  const int g0 = CH ? 4 * stripe_begin(cpa, nquad, P, 2) : 0;
+  const int cg = CH ? 4 * stripe_begin(cpb, nquad, P, 2) - g0 : ngroups;
+
+  // ---- activations, step 1: this lane's bf16 inputs (unit u = (token u / cg, group g0 + u % cg)), requested and
+  // waited for before any weight request
+  const int sub = lane % LPU, units = cg * mm, ustride = nwv * UPW;  // real tokens only (padding rows unused)
   const int u0 = wave * UPW + lane / LPU;
   const int npass = (units + ustride - 1) / ustride;
   uint4 xv[XB];
   auto xload = [&](int pass0) {
 #pragma unroll
     for (int b = 0; b < XB; ++b) {
-      const int u = u0 + (pass0 + b) * ustride, t = u / ngroups, kk = (u - t * ngroups) * kG + 8 * sub;
+      const int u = u0 + (pass0 + b) * ustride, t = u / cg, kk = (g0 + u - t * cg) * kG + 8 * sub;
       const bool ok = u < units && t < mm && kk < k;
       xv[b] = make_uint4(0u, 0u, 0u, 0u);
       if (pass0 + b < npass) {
@@ -156,7 +183,7 @@ __global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
 
   // ---- this wave's tasks: stripe set j, quads [qa, qb), blocks b0w, b0w + bstep, ... < nb
   const int j = wave % SPLIT, bstep = nwv / SPLIT, b0w = wave / SPLIT;
-  const int pa = j * P / SPLIT, pb = (j + 1) * P / SPLIT;
+  const int pa = CH ? cpa : j * P / SPLIT, pb = CH ? cpb : (j + 1) * P / SPLIT;
   const int qa = stripe_begin(pa, nquad, P, 2), qb = stripe_begin(pb, nquad, P, 2);
   const int ntw = b0w < nb ? (nb - b0w + bstep - 1) / bstep : 0;
   const int nitems = ntw * (qb - qa);
@@ -225,7 +252,7 @@ __global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
       if (p0 + b >= npass || wave * UPW + (p0 + b) * ustride >= units) break;  // no unit of this wave (uniform)
       const int u = u0 + (p0 + b) * ustride;
       const bool live = u < units;
-      const int t = live ? u / ngroups : 0, g = live ? u - t * ngroups : 0, tg = t >> 2, ui = t & 3;
+      const int t = live ? u / cg : 0, g = live ? u - t * cg : 0, tg = t >> 2, ui = t & 3;  // g: of the chunk
       const int eg0 = 8 * sub, ch = eg0 >> 5;
       int b0, b1, b2;
       const int e = convert_unit<BITS>(xv[b], ximg + ((g * 2) * NT + tg) * 768 + ch * 192 + ui * 48, NT * 768,
@@ -234,7 +261,7 @@ __global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
         if (sub == 0) {
           constexpr int OFF = code_offset<BITS>();
           const i32x4 mv = {-OFF * b0, -OFF * b1, -OFF * b2, act_scale_bits(e)};
-          meta[(tg * ngroups + g) * 4 + ui] = mv;
+          meta[(tg * cgs + g) * 4 + ui] = mv;
         }
       }
     }
@@ -281,10 +308,10 @@ __global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
     for (int s = 0; s < 4; ++s) {
       i32x4 b0, b1;
       make_b<BITS>(rq[s], b0, b1);
-      const int g = 4 * cq + s;
+      const int g = 4 * cq + s - g0;  // group of the chunk's image
 #pragma unroll
       for (int tg = 0; tg < NT; ++tg) {
-        const i32x4 mt = meta[(tg * ngroups + g) * 4 + h];
+        const i32x4 mt = meta[(tg * cgs + g) * 4 + h];
         const uint8_t* src = lds + a_lane + g * a_gmul + tg * a_tmul;
         const i32x4 a0 = *reinterpret_cast<const i32x4*>(src);
         const i32x4 a1 = *reinterpret_cast<const i32x4*>(src + a_hmul);
@@ -314,7 +341,10 @@ __global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
     float pp[NT];
 #pragma unroll
     for (int tg = 0; tg < NT; ++tg) pp[tg] = ((v[tg][0] + v[tg][1]) + v[tg][2]) + v[tg][3];
-    if constexpr (SPLIT == 1) {
+    if constexpr (CH) {  // added in stripe order after the last chunk
+#pragma unroll
+      for (int tg = 0; tg < NT; ++tg) part[((eg * P + ep) * MP + 4 * tg + h) * 16 + c] = pp[tg];
+    } else if constexpr (SPLIT == 1) {
 #pragma unroll
       for (int tg = 0; tg < NT; ++tg) {
         yrun[tg] = ep == 0 ? pp[tg] : yrun[tg] + pp[tg];
@@ -366,7 +396,23 @@ __global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
       if (e) stripe_end(v, g, p);
     }
   }
+  if constexpr (CH) __syncthreads();  // the chunk's image is free, its partials are in
+  };
+  if constexpr (CH) {
+    for (int ch = 0; ch < nch; ++ch) run_chunk(ch);
+  } else {
+    run_chunk(0);
+  }
   AK_M1_STAMP(3);
+  if constexpr (CH) {
+    for (int i = tid; i < nb * MP * 16; i += 64 * nwv) {
+      const int bl = i / (MP * 16), o = i - bl * MP * 16;
+      const float* slot = part + bl * P * MP * 16;
+      float y = slot[o];
+      for (int q = 1; q < P; ++q) y += slot[q * MP * 16 + o];
+      yl[i] = f2bf(y);
+    }
+  }
   __syncthreads();
   for (int i = tid; i < nb * MP * 16; i += 64 * nwv) {
     const int bl = i / (MP * 16), t = (i / 16) % MP, row = (b_lo + bl) * 16 + (i & 15);
@@ -378,20 +424,28 @@ size_t mt_block_bytes(int P, int split, int nt) {  // per 16-row block: outputs,
   return (size_t)4 * nt * 16 * 2 + (split > 1 ? (size_t)P * 4 * nt * 16 * 4 + 4 : 0);
 }
 
-template <int BITS, int SPLIT, int NT>
+template <int BITS, int SPLIT, int NT, bool CH>
 void launch_mt_split(const I8Args& a, int grid, size_t smem, hipStream_t s) {
   constexpr int DEPTH = 2;
-  hipLaunchKernelGGL((i8_mt_kernel<BITS, SPLIT, DEPTH, NT>), dim3(grid), dim3(1024), smem, s, a);
+  hipLaunchKernelGGL((i8_mt_kernel<BITS, SPLIT, DEPTH, NT, CH>), dim3(grid), dim3(1024), smem, s, a);
+}
+
+// groups of the largest of nch chunks of stripes
+int mt_chunk_groups(int nquad, int P, int nch) {
+  int cg = 0;
+  for (int q = 0; q < nch; ++q) {
+    const int gq = 4 * (stripe_begin((q + 1) * P / nch, nquad, P, 2) - stripe_begin(q * P / nch, nquad, P, 2));
+    cg = gq > cg ? gq : cg;
+  }
+  return cg;
 }
 
 template <int BITS, int NT>
 int launch_mt(I8Args a, hipStream_t s) {
   const Segs& g = a.segs;
   const int ngroups = a.nquad * 4, ntile = a.nquad / 2;
-  const size_t x_bytes = 256 + (size_t)mt_a_bytes(ngroups, NT) + mt_meta_bytes(ngroups, NT);
   for (int i = 0; i < g.nseg; ++i)  // buffer offsets are 32-bit
     if ((long long)ntile * g.n[i] * 128 * BITS >= (1ll << 31)) return AK_INVALID;
-  if (x_bytes > 140 * 1024) return AK_INVALID;
   // workgroups per segment: about the same number of 16-row blocks each, at most one workgroup per CU
   int total = 0;
   for (int i = 0; i < g.nseg; ++i) total += (g.n[i] + 15) / 16;
@@ -411,38 +465,58 @@ int launch_mt(I8Args a, hipStream_t s) {
     const int nbs = (g.n[i] + 15) / 16, gs = (nbs + per - 1) / per;
     nbmax = (nbs + gs - 1) / gs > nbmax ? (nbs + gs - 1) / gs : nbmax;
   }
-  // tasks per block: fewest quad rounds for the busiest wave, a task's overhead counted as about one quad
-  int best_split = 1;
-  double best = 1e30;
-  for (int split : {1, 2, 4, 8}) {
-    if (split > a.P) break;
-    if (x_bytes + (size_t)nbmax * mt_block_bytes(a.P, split, NT) + 16 > 160 * 1024) continue;
-    int lmax = 0;
-    for (int j = 0; j < split; ++j) {
-      const int l = stripe_begin((j + 1) * a.P / split, a.nquad, a.P, 2) - stripe_begin(j * a.P / split, a.nquad, a.P, 2);
-      lmax = l > lmax ? l : lmax;
+  const size_t x_bytes = 256 + (size_t)mt_a_bytes(ngroups, NT) + mt_meta_bytes(ngroups, NT);
+  if (x_bytes <= 140 * 1024) {
+    // the whole activation image fits: tasks per block = fewest quad rounds for the busiest wave, a task's overhead
+    // counted as about one quad
+    int best_split = 1;
+    double best = 1e30;
+    for (int split : {1, 2, 4, 8}) {
+      if (split > a.P) break;
+      if (x_bytes + (size_t)nbmax * mt_block_bytes(a.P, split, NT) + 16 > 160 * 1024) continue;
+      int lmax = 0;
+      for (int j = 0; j < split; ++j) {
+        const int l = stripe_begin((j + 1) * a.P / split, a.nquad, a.P, 2) - stripe_begin(j * a.P / split, a.nquad, a.P, 2);
+        lmax = l > lmax ? l : lmax;
+      }
+      const int bstep = 16 / split;
+      const double cost = (double)((nbmax + bstep - 1) / bstep) * (lmax + 1.0);
+      if (cost < best - 1e-9) best = cost, best_split = split;
     }
-    const int bstep = 16 / split;
-    const double cost = (double)((nbmax + bstep - 1) / bstep) * (lmax + 1.0);
-    if (cost < best - 1e-9) best = cost, best_split = split;
+    if (best < 1e29) {
+      const size_t smem = x_bytes + (size_t)nbmax * mt_block_bytes(a.P, best_split, NT) + 16;
+      switch (best_split) {
+        case 1: launch_mt_split<BITS, 1, NT, false>(a, grid, smem, s); break;
+        case 2: launch_mt_split<BITS, 2, NT, false>(a, grid, smem, s); break;
+        case 4: launch_mt_split<BITS, 4, NT, false>(a, grid, smem, s); break;
+        default: launch_mt_split<BITS, 8, NT, false>(a, grid, smem, s); break;
+      }
+      return (int)hipGetLastError();
+    }
   }
-  if (best > 1e29) return AK_INVALID;
-  const size_t smem = x_bytes + (size_t)nbmax * mt_block_bytes(a.P, best_split, NT) + 16;
-  switch (best_split) {
-    case 1: launch_mt_split<BITS, 1, NT>(a, grid, smem, s); break;
-    case 2: launch_mt_split<BITS, 2, NT>(a, grid, smem, s); break;
-    case 4: launch_mt_split<BITS, 4, NT>(a, grid, smem, s); break;
-    default: launch_mt_split<BITS, 8, NT>(a, grid, smem, s); break;
+  // chunked: the fewest chunks of stripes whose image, with every block's stripe partials, fits the LDS
+  const size_t blk = (size_t)4 * NT * 16 * 2 + (size_t)a.P * 4 * NT * 16 * 4;
+  for (int nch = 2; nch <= a.P; ++nch) {
+    const int cg = mt_chunk_groups(a.nquad, a.P, nch);
+    const size_t smem = 256 + (size_t)mt_a_bytes(cg, NT) + mt_meta_bytes(cg, NT) + (size_t)nbmax * blk + 16;
+    if (smem > 160 * 1024) continue;
+    a.nb = nch;
+    launch_mt_split<BITS, 1, NT, true>(a, grid, smem, s);
+    return (int)hipGetLastError();
   }
-  return (int)hipGetLastError();
+  return AK_INVALID;
 }
 
 }  // namespace
 
-// 2..8 tokens (4 or 8 in the kernel; the dispatcher sends 3..8), 16-row blocks (the last one padded).  Returns AK_INVALID if the shape does not
-// suit the kernel (group 64, the tokens' activations beyond the LDS, a segment beyond 2 GB): the caller falls back.
+// 1..8 tokens (4 or 8 in the kernel), 16-row blocks (the last one padded); activations beyond the LDS in chunks of
+// stripes.  Returns AK_INVALID if the shape does not suit the kernel (group 64, a segment beyond 2 GB, a chunk of
+// one stripe beyond the LDS): the caller falls back.
 int i8_gemv_mt(int bits, const void* x, int m, const Segs& g, int k, int group, hipStream_t s) {
-  if (group != kG || m < 2 || m > 8) return AK_INVALID;
+  if (group != kG || m < 1 || m > 8) return AK_INVALID;
+#ifdef AK_NO_MT
+  return AK_INVALID;
+#endif
   I8Args a;
   a.segs = g;
   a.x = static_cast<const uint16_t*>(x);
