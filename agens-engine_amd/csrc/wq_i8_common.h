@@ -13,6 +13,8 @@ struct I8Args {
   int qpt;        // quads per 1024-input tile (2 for group 128, 4 for group 64)
   int nb;         // quads per LDS batch (any-m kernel)
   int wg_end[4];  // m = 1 kernel: workgroups of segments 0..i (each workgroup serves one segment)
+  float* part;    // split-K launches: stripe partials [P][tokens][rows] and, at cnt, one counter per row range
+  int* cnt;
 };
 
 // Stripes are contiguous runs of whole 1024-input tiles: with nt = nquad / qpt tiles, P = min(8, nt) stripes and stripe

@@ -38,12 +38,14 @@
 namespace agq {
 
 int num_cus();
+void* stream_scratch(hipStream_t s, size_t bytes);
 
 namespace {
 
 constexpr int kG = 128;
 constexpr int kRsrcWord3 = 0x00020000;  // raw buffer resource, dword 3 (CDNA)
 constexpr int kNt = 2;                    // streaming (non-temporal) cache policy for the weights
+constexpr int kVmcnt0 = 0x0F70;            // s_waitcnt immediate: vector memory counter 0, the others unconstrained
 
 // one item of one lane: the raw weight words of the quad's four groups (W2 / W3: before the lane exchange) and the
 // scales of its row for the four groups
@@ -96,9 +98,14 @@ __host__ __device__ inline int mt_meta_bytes(int ngroups, int nt) { return nt * 
 // CH: the stripes are processed in a.nb chunks one after the other (all waves on one chunk's stripes, each chunk with
 // its own activation image), for activations beyond the LDS; stripe partials wait in the LDS and are added in stripe
 // order at the end, so the results are those of an unchunked launch.
-template <int BITS, int SPLIT, int DEPTH, int NT, bool CH>
+//
+// SK (split-K across workgroups, for activations beyond the LDS, one segment): workgroup (r, p) computes stripe p of the
+// rows of range r, converting only that stripe's activations; it writes its stripe partials with device-coherent
+// stores, and the last of the range's P workgroups (device-scope counter) adds them in stripe order and writes y.
+template <int BITS, int SPLIT, int DEPTH, int NT, bool CH, bool SK = false>
 __global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
-  static_assert(!CH || SPLIT == 1, "a chunked launch gives every wave whole stripes of its blocks");
+  static_assert((!CH && !SK) || SPLIT == 1, "chunked and split launches give every wave whole stripes of its blocks");
+  static_assert(!(CH && SK), "one of the two");
   extern __shared__ __attribute__((aligned(256))) uint8_t lds[];
   constexpr int LPU = kG / 8, UPW = 64 / LPU, XB = 4, MP = 4 * NT;  // MP: padded tokens
   constexpr int REC = 128 * BITS;
@@ -109,11 +116,13 @@ __global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const Segs& sgs = a.segs;
 
-  // this workgroup's segment and its 16-row blocks [b_lo, b_lo + nb) of that segment
+  // this workgroup's segment and its 16-row blocks [b_lo, b_lo + nb) of that segment (SK: row range r, stripe psk)
   int sg = 0;
 #pragma unroll
   for (int i = 1; i < kMaxSegs; ++i) sg += (i < sgs.nseg && (int)blockIdx.x >= a.wg_end[i - 1]) ? 1 : 0;
-  const int wg0 = sg ? AK_PICK(sg - 1, a.wg_end) : 0, gs = AK_PICK(sg, a.wg_end) - wg0, w = blockIdx.x - wg0;
+  const int nr = SK ? (int)gridDim.x / P : 1, r = SK ? (int)blockIdx.x / P : 0, psk = SK ? (int)blockIdx.x - r * P : 0;
+  const int wg0 = sg ? AK_PICK(sg - 1, a.wg_end) : 0, gs = SK ? nr : AK_PICK(sg, a.wg_end) - wg0;
+  const int w = SK ? r : (int)blockIdx.x - wg0;
   const int n = AK_PICK(sg, sgs.n), n_b16 = (n + 15) >> 4;
   const int b_lo = (int)((long long)w * n_b16 / gs);
   const int nb = (int)((long long)(w + 1) * n_b16 / gs) - b_lo;
@@ -123,6 +132,7 @@ __global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
   // chunks of stripes and the groups an activation image holds (the largest chunk's)
   const int nch = CH ? a.nb : 1;
   int cgs = ngroups;
+  if constexpr (SK) cgs = 4 * (stripe_begin(psk + 1, nquad, P, 2) - stripe_begin(psk, nquad, P, 2));
   if constexpr (CH) {
     cgs = 0;
     for (int q = 0; q < nch; ++q) {
@@ -153,9 +163,9 @@ __global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
   if constexpr (CH) asm volatile("" : "+v"(tidc));
   const int lane = tidc & 63, c = lane & 15, h = lane >> 4;
   // this chunk: stripes [cpa, cpb), groups [g0, g0 + cg) (the whole k unless CH)
-  const int cpa = CH ? ch * P / nch : 0, cpb = CH ? (ch + 1) * P / nch : P;
-  const int g0 = CH ? 4 * stripe_begin(cpa, nquad, P, 2) : 0;
-  const int cg = CH ? 4 * stripe_begin(cpb, nquad, P, 2) - g0 : ngroups;
+  const int cpa = CH ? ch * P / nch : SK ? psk : 0, cpb = CH ? (ch + 1) * P / nch : SK ? psk + 1 : P;
+  const int g0 = CH || SK ? 4 * stripe_begin(cpa, nquad, P, 2) : 0;
+  const int cg = CH || SK ? 4 * stripe_begin(cpb, nquad, P, 2) - g0 : ngroups;
 
   // ---- activations, step 1: this lane's bf16 inputs (unit u = (token u / cg, group g0 + u % cg)), requested and
   // waited for before any weight request
@@ -183,7 +193,7 @@ __global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
 
   // ---- this wave's tasks: stripe set j, quads [qa, qb), blocks b0w, b0w + bstep, ... < nb
   const int j = wave % SPLIT, bstep = nwv / SPLIT, b0w = wave / SPLIT;
-  const int pa = CH ? cpa : j * P / SPLIT, pb = CH ? cpb : (j + 1) * P / SPLIT;
+  const int pa = CH || SK ? cpa : j * P / SPLIT, pb = CH || SK ? cpb : (j + 1) * P / SPLIT;
   const int qa = stripe_begin(pa, nquad, P, 2), qb = stripe_begin(pb, nquad, P, 2);
   const int ntw = b0w < nb ? (nb - b0w + bstep - 1) / bstep : 0;
   const int nitems = ntw * (qb - qa);
@@ -344,6 +354,11 @@ __global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
     if constexpr (CH) {  // added in stripe order after the last chunk
 #pragma unroll
       for (int tg = 0; tg < NT; ++tg) part[((eg * P + ep) * MP + 4 * tg + h) * 16 + c] = pp[tg];
+    } else if constexpr (SK) {  // to the range's partials, device-coherent (the range's last workgroup adds them)
+#pragma unroll
+      for (int tg = 0; tg < NT; ++tg)
+        __hip_atomic_store(a.part + ((size_t)(ep * MP + 4 * tg + h) * n_b16 + b_lo + eg) * 16 + c, pp[tg],
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     } else if constexpr (SPLIT == 1) {
 #pragma unroll
       for (int tg = 0; tg < NT; ++tg) {
@@ -404,6 +419,28 @@ __global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
     run_chunk(0);
   }
   AK_M1_STAMP(3);
+  if constexpr (SK) {
+    // every wave's partial stores are acknowledged at device scope before the range's counter moves
+    __builtin_amdgcn_s_waitcnt(kVmcnt0);
+    __syncthreads();
+    int* const last = reinterpret_cast<int*>(yl);
+    if (tid == 0) {
+      const int old = __hip_atomic_fetch_add(a.cnt + r, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      *last = old == P - 1;
+      if (old == P - 1) __hip_atomic_store(a.cnt + r, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next launch
+    }
+    __syncthreads();
+    if (!*last) return;
+    __syncthreads();  // every thread has read the flag before the outputs overwrite it
+    for (int i = tid; i < nb * MP * 16; i += 64 * nwv) {
+      const int bl = i / (MP * 16), o = i - bl * MP * 16, t = o >> 4;
+      const float* src = a.part + ((size_t)t * n_b16 + b_lo + bl) * 16 + (o & 15);
+      float y = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (int q = 1; q < P; ++q)
+        y += __hip_atomic_load(src + (size_t)q * MP * n_b16 * 16, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      yl[i] = f2bf(y);
+    }
+  }
   if constexpr (CH) {
     for (int i = tid; i < nb * MP * 16; i += 64 * nwv) {
       const int bl = i / (MP * 16), o = i - bl * MP * 16;
@@ -424,10 +461,10 @@ size_t mt_block_bytes(int P, int split, int nt) {  // per 16-row block: outputs,
   return (size_t)4 * nt * 16 * 2 + (split > 1 ? (size_t)P * 4 * nt * 16 * 4 + 4 : 0);
 }
 
-template <int BITS, int SPLIT, int NT, bool CH>
+template <int BITS, int SPLIT, int NT, bool CH, bool SK = false>
 void launch_mt_split(const I8Args& a, int grid, size_t smem, hipStream_t s) {
   constexpr int DEPTH = 2;
-  hipLaunchKernelGGL((i8_mt_kernel<BITS, SPLIT, DEPTH, NT, CH>), dim3(grid), dim3(1024), smem, s, a);
+  hipLaunchKernelGGL((i8_mt_kernel<BITS, SPLIT, DEPTH, NT, CH, SK>), dim3(grid), dim3(1024), smem, s, a);
 }
 
 // groups of the largest of nch chunks of stripes
@@ -494,6 +531,21 @@ int launch_mt(I8Args a, hipStream_t s) {
       return (int)hipGetLastError();
     }
   }
+  // split-K across workgroups (one segment): P workgroups per row range, each one stripe, partials in the stream's
+  // scratch; without scratch (inside a capture that has not got it yet) the chunked launch below
+  if (g.nseg == 1 && a.P >= 2) {
+    const int cus = num_cus(), nr = cus / a.P > 0 ? cus / a.P : 1, nbs = (g.n[0] + 15) / 16;
+    const int nbr = (nbs + nr - 1) / nr, cg = mt_chunk_groups(a.nquad, a.P, a.P);
+    const size_t smem = 256 + (size_t)mt_a_bytes(cg, NT) + mt_meta_bytes(cg, NT) + (size_t)nbr * 4 * NT * 16 * 2 + 16;
+    const size_t cnt_bytes = 4096, part_bytes = (size_t)a.P * 4 * NT * nbs * 16 * 4;
+    void* z = nr <= 1024 && smem <= 160 * 1024 ? stream_scratch(s, cnt_bytes + part_bytes) : nullptr;
+    if (z) {
+      a.cnt = static_cast<int*>(z);
+      a.part = reinterpret_cast<float*>(static_cast<uint8_t*>(z) + cnt_bytes);
+      launch_mt_split<BITS, 1, NT, false, true>(a, nr * a.P, smem, s);
+      return (int)hipGetLastError();
+    }
+  }
   // chunked: the fewest chunks of stripes whose image, with every block's stripe partials, fits the LDS
   const size_t blk = (size_t)4 * NT * 16 * 2 + (size_t)a.P * 4 * NT * 16 * 4;
   for (int nch = 2; nch <= a.P; ++nch) {
@@ -526,6 +578,8 @@ int i8_gemv_mt(int bits, const void* x, int m, const Segs& g, int k, int group, 
   a.qpt = 2;
   a.P = stripe_count(a.nquad, a.qpt);
   a.nb = 0;
+  a.part = nullptr;
+  a.cnt = nullptr;
   const int nt = m <= 4 ? 1 : 2;
   switch (bits * 10 + nt) {
     case 41: return launch_mt<4, 1>(a, s);

@@ -3,6 +3,10 @@
 // The KT byte layout is the reference's (kernels/src/w4_gemv.cu:13-31, :439-458, :758-790) so weights repacked here
 // are interchangeable with the reference's; the kernels are written for wave64: one thread per 16-byte lane chunk of
 // the output, consecutive threads writing consecutive chunks of a record (fully coalesced stores), grid-stride loops.
+#include <map>
+#include <mutex>
+#include <utility>
+
 #include "agens_kernels.h"
 #include "wq_common.h"
 
@@ -17,6 +21,40 @@ int num_cus() {
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 256;
   }
   return cus;
+}
+
+// Library scratch per (device, stream), as the reference keeps its split-K partials and counters
+// (w4_gemv.cu:2096-2118): allocated zero-filled on first use and grown when a launch needs more, never inside a stream
+// capture (null then: the caller takes a path without scratch), held until the process ends.  Launches on one stream
+// are ordered, so they share it safely; before a buffer is replaced the stream is synchronized (earlier launches may
+// still use it).  Users keep their counters at zero between launches.
+void* stream_scratch(hipStream_t s, size_t bytes) {
+  static std::mutex mu;
+  static std::map<std::pair<int, hipStream_t>, std::pair<void*, size_t>> bufs;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  std::lock_guard<std::mutex> lock(mu);
+  auto& b = bufs[{dev, s}];
+  if (b.first && b.second >= bytes) return b.first;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  const size_t want = bytes > ((size_t)4 << 20) ? bytes : ((size_t)4 << 20);
+  if (b.first) {
+    (void)hipStreamSynchronize(s);
+    (void)hipFree(b.first);
+    b = {nullptr, 0};
+  }
+  void* p = nullptr;
+  if (hipMalloc(&p, want) != hipSuccess || hipMemset(p, 0, want) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+    if (p) (void)hipFree(p);
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  b = {p, want};
+  return p;
 }
 
 namespace {

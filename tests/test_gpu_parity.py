@@ -273,3 +273,31 @@ def test_baseline_config_shapes(cfg):
     s_sub = scales.reshape(n, k // g)[sub].ravel()
     ref32 = ora_ref_f32(x, 1, p_sub, s_sub, 256, k, g)
     assert max_rel_excess(y1[:, sub], ref32) <= 2e-3
+
+
+@pytest.mark.parametrize("bits", [4, 3, 2])
+@pytest.mark.parametrize("m", [2, 3, 4, 5, 8])
+def test_long_k_small_m(bits, m):
+    """Activations beyond the LDS at 2..8 tokens: one segment (split-K across workgroups, stripe partials added by each
+    row range's last workgroup) and two segments (chunks of stripes in one workgroup).  Rows equal the oracle and the
+    one-token launches; a second launch repeats the first (the split's counters return to zero)."""
+    K = kernels()
+    k, g = 27648, 128
+    A = make_linear(970 + bits, 900, k, g, bits)
+    Bl = make_linear(980 + bits, 136, k, g, bits)
+    x = gen_x(990 + m, m * k)
+    X = Dev.of(x)
+    y1 = y_of(gemv(bits, X, m, [A], k, g)[0], m, 900)
+    y1b = y_of(gemv(bits, X, m, [A], k, g)[0], m, 900)
+    assert np.array_equal(y1, y1b)
+    ya, yb = gemv(bits, X, m, [A, Bl], k, g)
+    assert np.array_equal(y_of(ya, m, 900), y1)
+    wt, st = A.host_kt()
+    wtb, stb = Bl.host_kt()
+    for r0 in (0, 448, 900 - 40):
+        yo = ora_fast(bits, x, m, wt, st, 900, k, g, rows=(r0, r0 + 40))
+        assert (y1[:, r0:r0 + 40] == yo[:, r0:r0 + 40]).all(), f"rows {r0}"
+    assert (y_of(yb, m, 136) == ora_fast(bits, x, m, wtb, stb, 136, k, g)).all()
+    for j in (0, m - 1):
+        one = y_of(gemv(bits, X.addr(j * k * 2), 1, [A], k, g)[0], 1, 900)[0]
+        assert (one == y1[j]).all()
