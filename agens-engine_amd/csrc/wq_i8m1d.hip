@@ -56,6 +56,7 @@
 namespace agq {
 
 int num_cus();
+void* stream_scratch(hipStream_t s, size_t bytes);
 
 namespace {
 
@@ -174,8 +175,13 @@ __device__ __forceinline__ void lds_barrier() {
 // One GEMV step of one workgroup.  CHAIN: part of a chained launch (workgroups past the step's grid return at once;
 // with `wait`, the step waits for all workgroups to reach `target` after its first weight requests; activations are
 // read and outputs written device-coherently).
-template <int BITS, int SPLIT, int DEPTH, int MT, bool CHAIN>
+//
+// SK (split-K across workgroups, one segment): workgroup (r, p) computes stripe p of the rows of range r, converting
+// only that stripe's activations; it writes its stripe partials with device-coherent stores, and the last of the
+// range's P workgroups (device-scope counter) adds them in stripe order and writes y.
+template <int BITS, int SPLIT, int DEPTH, int MT, bool CHAIN, bool SK = false>
 __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wait, uint32_t target, int ps = 0) {
+  static_assert(!SK || SPLIT == 1, "a split launch gives every wave whole stripes of its blocks");
   AK_PROBE(ps, 0);
   constexpr int LPU = kG / 8, UPW = 64 / LPU, XB = 4;
   constexpr int REC = 128 * BITS;  // one row's tile record
@@ -193,12 +199,18 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
   const Segs& sgs = a.segs;
 
   if (CHAIN && (int)blockIdx.x >= AK_PICK(sgs.nseg - 1, a.wg_end)) return;  // no rows of this step
-  // this workgroup's segment and its blocks [b_lo, b_lo + nb) of that segment
+  // this workgroup's segment and its blocks [b_lo, b_lo + nb) of that segment (SK: row range r, stripe psk; the
+  // ranges are wg_end[0] / P)
   int sg = 0;
 #pragma unroll
   for (int i = 1; i < kMaxSegs; ++i) sg += (i < sgs.nseg && (int)blockIdx.x >= a.wg_end[i - 1]) ? 1 : 0;
-  const int wg0 = sg ? AK_PICK(sg - 1, a.wg_end) : 0, gs = AK_PICK(sg, a.wg_end) - wg0, w = blockIdx.x - wg0;
+  const int nr = SK ? a.wg_end[0] / P : 1, r = SK ? (int)blockIdx.x / P : 0, psk = SK ? (int)blockIdx.x - r * P : 0;
+  const int wg0 = sg ? AK_PICK(sg - 1, a.wg_end) : 0, gs = SK ? nr : AK_PICK(sg, a.wg_end) - wg0;
+  const int w = SK ? r : (int)blockIdx.x - wg0;
   const int n = AK_PICK(sg, sgs.n), n_b4 = (n + 3) >> 2;
+  // the quads the activation image holds: [q0, q0 + nqs) (SK: stripe psk; else all)
+  const int q0 = SK ? stripe_begin(psk, nquad, P, 2) : 0;
+  const int nqs = SK ? stripe_begin(psk + 1, nquad, P, 2) - q0 : nquad;
   const int b_lo = (int)((long long)w * n_b4 / gs);
   const int nb = (int)((long long)(w + 1) * n_b4 / gs) - b_lo;
   uint16_t* const yseg = AK_PICK(sg, sgs.y);
@@ -208,10 +220,10 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
   //      outputs [MT][nb][4] bf16 | partials [nb][P][MT][4] | tickets [nb]
   // (48-byte chunk stride: the 12 active lanes of each 16-lane pass of an A read hit 12 distinct 16-byte bank slots of
   // the 256-byte bank row, and the 4 zero-operand lanes read zeros placed in the 4 remaining slots)
-  const int tstride = nquad * kCPQ * 96;  // limbs of one token
+  const int tstride = nqs * kCPQ * 96;  // limbs of one token
   uint8_t* xq = lds + 512;
   i32x4* meta = reinterpret_cast<i32x4*>(xq + MT * tstride);
-  uint16_t* yl = reinterpret_cast<uint16_t*>(meta + MT * nquad * 4);
+  uint16_t* yl = reinterpret_cast<uint16_t*>(meta + MT * nqs * 4);
   float* part = reinterpret_cast<float*>(yl + ((MT * nb * 4 + 3) & ~3));
   int* tickets = reinterpret_cast<int*>(part + (SPLIT > 1 ? nb * P * MT * 4 : 0));
 
@@ -221,7 +233,7 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
 
   // ---- activations, step 1: this lane's bf16 inputs, requested and waited for before any weight request (behind
   // the weight requests of the whole GPU, x would arrive microseconds late)
-  const int gpt = nquad * 4;  // groups per token
+  const int gpt = nqs * 4;  // groups per token (of the image)
   const int sub = lane % LPU, units = gpt * MT, ustride = nwv * UPW;
   const int u0 = wave * UPW + lane / LPU;
   const int npass = (units + ustride - 1) / ustride;
@@ -233,7 +245,7 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
 #pragma unroll
     for (int b = 0; b < XB; ++b) {
       // lanes past the end load x[0] (zero-selected); passes past npass load nothing (a wave-uniform branch)
-      const int u = u0 + (pass0 + b) * ustride, t = MT == 1 ? 0 : u / gpt, kk = (u - t * gpt) * kG + 8 * sub;
+      const int u = u0 + (pass0 + b) * ustride, t = MT == 1 ? 0 : u / gpt, kk = (4 * q0 + u - t * gpt) * kG + 8 * sub;
       const bool ok = u < units && t < mm && kk < k;
       xv[b] = make_uint4(0u, 0u, 0u, 0u);
       if (pass0 + b < npass) {
@@ -259,7 +271,7 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
 
   // ---- this wave's tasks: stripe set j, tiles [ta, tb), blocks b0w, b0w + bstep, ... < nb
   const int j = wave % SPLIT, bstep = nwv / SPLIT, b0w = wave / SPLIT;
-  const int pa = j * P / SPLIT, pb = (j + 1) * P / SPLIT;
+  const int pa = SK ? psk : j * P / SPLIT, pb = SK ? psk + 1 : (j + 1) * P / SPLIT;
   const int ta = stripe_begin(pa, nquad, P, 2) >> 1, tb = stripe_begin(pb, nquad, P, 2) >> 1;
   const int ntw = b0w < nb ? (nb - b0w + bstep - 1) / bstep : 0;
   const int nitems = ntw * (tb - ta);
@@ -398,8 +410,8 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
       // token by token: the activation operand and meta of one token are live at a time
 #pragma unroll
       for (int t = 0; t < MT; ++t) {
-        const i32x4 mt = meta[(t * nquad + cq) * 4 + h];
-        const uint8_t* src = lds + a_base + t * a_tmul + cq * a_qmul;
+        const i32x4 mt = meta[(t * nqs + cq - q0) * 4 + h];
+        const uint8_t* src = lds + a_base + t * a_tmul + (cq - q0) * a_qmul;
         const i32x4 a0 = *reinterpret_cast<const i32x4*>(src);
         const i32x4 a1 = *reinterpret_cast<const i32x4*>(src + (a_on ? kCPQ * 48 : 0));
         i32x4 d = mt;
@@ -434,7 +446,13 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
                   v3 = __int_as_float(__builtin_amdgcn_ds_bpermute(sl3, vi));
       pp[t] = ((v0 + v1) + v2) + v3;
     }
-    if constexpr (SPLIT == 1) {
+    if constexpr (SK) {  // to the range's partials, device-coherent (the range's last workgroup adds them)
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+        if (lane < 4)
+          __hip_atomic_store(a.part + ((size_t)(ep * MT + t) * n_b4 + b_lo + eg) * 4 + lane, pp[t], __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+    } else if constexpr (SPLIT == 1) {
 #pragma unroll
       for (int t = 0; t < MT; ++t) {
         yrun[t] = ep == 0 ? pp[t] : yrun[t] + pp[t];
@@ -493,6 +511,28 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
   AK_PROBE_W(ps, 2);
   __syncthreads();
   AK_PROBE(ps, 3);
+  if constexpr (SK) {
+    // every wave's partial stores are acknowledged at device scope before the range's counter moves
+    __builtin_amdgcn_s_waitcnt(kVmcnt0);
+    __syncthreads();
+    int* const last = reinterpret_cast<int*>(lds);  // the zeros are no longer read
+    if (tid == 0) {
+      const int old = __hip_atomic_fetch_add(a.cnt + r, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      *last = old == P - 1;
+      if (old == P - 1) __hip_atomic_store(a.cnt + r, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next launch
+    }
+    __syncthreads();
+    if (!*last) return;
+    for (int i = tid; i < MT * nb * 4; i += 64 * nwv) {
+      const int t = MT == 1 ? 0 : i / (nb * 4), o = i - t * nb * 4;
+      const float* src = a.part + ((size_t)t * n_b4 + b_lo) * 4 + o;
+      float y = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (int q = 1; q < P; ++q)
+        y += __hip_atomic_load(src + (size_t)q * MT * n_b4 * 4, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      yl[i] = f2bf(y);
+    }
+    __syncthreads();
+  }
   for (int i = tid; i < MT * nb * 4; i += 64 * nwv) {
     const int t = MT == 1 ? 0 : i / (nb * 4), row = b_lo * 4 + i - t * nb * 4;
     if (t < mm && row < n) {
@@ -504,11 +544,11 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
   }
 }
 
-template <int BITS, int SPLIT, int DEPTH, int MT>
+template <int BITS, int SPLIT, int DEPTH, int MT, bool SK = false>
 __global__ void __launch_bounds__(1024, 1) i8_m1d_kernel(const I8Args a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   AK_M1_WG_BEGIN();
-  m1d_body<BITS, SPLIT, DEPTH, MT, false>(a, lds, false, 0u);
+  m1d_body<BITS, SPLIT, DEPTH, MT, false, SK>(a, lds, false, 0u);
   AK_M1_WG_END();
 }
 
@@ -585,8 +625,38 @@ void launch_split(const I8Args& a, int grid, int nwv, size_t smem, hipStream_t s
   hipLaunchKernelGGL((i8_m1d_kernel<BITS, SPLIT, m1d_depth(MT), MT>), dim3(grid), dim3(64 * nwv), smem, s, a);
 }
 
+// split-K across workgroups (one segment, 8 stripes, k of at least AK_M1_SK_QUADS quads): P workgroups per row range,
+// each one stripe; partials and counters in the stream's scratch.  0: not launched (no scratch inside a capture, or
+// the shape does not suit it).
+#ifndef AK_M1_SK_QUADS
+#define AK_M1_SK_QUADS 32
+#endif
+template <int BITS, int MT>
+int launch_m1d_sk(I8Args a, hipStream_t s) {
+  if constexpr (MT > 2) return AK_INVALID;  // 3..8 tokens: the tokens-in-A-rows kernel has its own split
+  const Segs& g = a.segs;
+  if (g.nseg != 1 || a.P != 8 || a.nquad < AK_M1_SK_QUADS) return AK_INVALID;
+  if ((long long)(a.nquad / 2) * g.n[0] * 128 * BITS >= (1ll << 31)) return AK_INVALID;
+  const int cus = num_cus(), nr = cus / a.P, nb4 = (g.n[0] + 3) / 4, nbr = (nb4 + nr - 1) / nr;
+  int nqs = 0;
+  for (int p = 0; p < a.P; ++p) {
+    const int q = stripe_begin(p + 1, a.nquad, a.P, 2) - stripe_begin(p, a.nquad, a.P, 2);
+    nqs = q > nqs ? q : nqs;
+  }
+  const size_t smem = m1d_x_bytes(nqs, MT) + (size_t)nbr * m1d_block_bytes(a.P, 1, MT) + 16;
+  if (nr < 1 || nr > 1024 || smem > 160 * 1024) return AK_INVALID;
+  void* z = stream_scratch(s, 4096 + (size_t)a.P * MT * nb4 * 4 * 4);
+  if (!z) return AK_INVALID;
+  a.cnt = static_cast<int*>(z);
+  a.part = reinterpret_cast<float*>(static_cast<uint8_t*>(z) + 4096);
+  a.wg_end[0] = nr * a.P;
+  hipLaunchKernelGGL((i8_m1d_kernel<BITS, 1, m1d_depth(MT), MT, true>), dim3(nr * a.P), dim3(1024), smem, s, a);
+  return (int)hipGetLastError();
+}
+
 template <int BITS, int MT>
 int launch_m1d(I8Args a, hipStream_t s) {
+  if (launch_m1d_sk<BITS, MT>(a, s) != AK_INVALID) return (int)hipGetLastError();
   M1dShape sh;
   if (plan_m1d(a, BITS, MT, false, sh)) return AK_INVALID;
   switch (sh.split) {
@@ -655,6 +725,8 @@ int i8_gemv_m1(int bits, const void* x, int m, const Segs& g, int k, int group, 
   a.qpt = 2;
   a.P = stripe_count(a.nquad, a.qpt);
   a.nb = 0;
+  a.part = nullptr;
+  a.cnt = nullptr;
   const int mt = m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8;
   switch (bits * 10 + mt) {
     case 41: return launch_m1d<4, 1>(a, s);
@@ -699,6 +771,8 @@ int m1d_chain_make(int nsteps, const int* bits, const void* const* x, const int*
     a.qpt = 2;
     a.P = stripe_count(a.nquad, a.qpt);
     a.nb = 0;
+    a.part = nullptr;
+    a.cnt = nullptr;
     M1dShape sh;
     if (plan_m1d(a, bits[i], mt, true, sh)) {
       free(h);
