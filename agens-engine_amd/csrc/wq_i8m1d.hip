@@ -35,6 +35,8 @@
 // into stripe partials.
 #include <stdlib.h>
 
+#include <vector>
+
 #include "agens_kernels.h"
 #include "wq_common.h"
 #include "wq_i8_common.h"
@@ -631,21 +633,33 @@ void launch_split(const I8Args& a, int grid, int nwv, size_t smem, hipStream_t s
 #ifndef AK_M1_SK_QUADS
 #define AK_M1_SK_QUADS 32
 #endif
-template <int BITS, int MT>
-int launch_m1d_sk(I8Args a, hipStream_t s) {
-  if constexpr (MT > 2) return AK_INVALID;  // 3..8 tokens: the tokens-in-A-rows kernel has its own split
+// the split-K shape of a launch: row ranges nr, LDS bytes and scratch bytes (4 KB of counters, then the partials);
+// false if the launch does not suit it
+bool m1d_sk_shape(const I8Args& a, int bits, int mt, int* nr_out, size_t* smem_out, size_t* scratch_out) {
   const Segs& g = a.segs;
-  if (g.nseg != 1 || a.P != 8 || a.nquad < AK_M1_SK_QUADS) return AK_INVALID;
-  if ((long long)(a.nquad / 2) * g.n[0] * 128 * BITS >= (1ll << 31)) return AK_INVALID;
-  const int cus = num_cus(), nr = cus / a.P, nb4 = (g.n[0] + 3) / 4, nbr = (nb4 + nr - 1) / nr;
+  if (mt > 2 || g.nseg != 1 || a.P != 8 || a.nquad < AK_M1_SK_QUADS) return false;
+  if ((long long)(a.nquad / 2) * g.n[0] * 128 * bits >= (1ll << 31)) return false;
+  const int cus = num_cus(), nr = cus / a.P, nb4 = (g.n[0] + 3) / 4, nbr = nr > 0 ? (nb4 + nr - 1) / nr : 0;
   int nqs = 0;
   for (int p = 0; p < a.P; ++p) {
     const int q = stripe_begin(p + 1, a.nquad, a.P, 2) - stripe_begin(p, a.nquad, a.P, 2);
     nqs = q > nqs ? q : nqs;
   }
-  const size_t smem = m1d_x_bytes(nqs, MT) + (size_t)nbr * m1d_block_bytes(a.P, 1, MT) + 16;
-  if (nr < 1 || nr > 1024 || smem > 160 * 1024) return AK_INVALID;
-  void* z = stream_scratch(s, 4096 + (size_t)a.P * MT * nb4 * 4 * 4);
+  const size_t smem = m1d_x_bytes(nqs, mt) + (size_t)nbr * m1d_block_bytes(a.P, 1, mt) + 16;
+  if (nr < 1 || nr > 1024 || smem > 160 * 1024) return false;
+  *nr_out = nr;
+  *smem_out = smem;
+  *scratch_out = 4096 + (size_t)a.P * mt * nb4 * 4 * 4;
+  return true;
+}
+
+template <int BITS, int MT>
+int launch_m1d_sk(I8Args a, hipStream_t s) {
+  if constexpr (MT > 2) return AK_INVALID;  // 3..8 tokens: the tokens-in-A-rows kernel has its own split
+  int nr = 0;
+  size_t smem = 0, zb = 0;
+  if (!m1d_sk_shape(a, BITS, MT, &nr, &smem, &zb)) return AK_INVALID;
+  void* z = stream_scratch(s, zb);
   if (!z) return AK_INVALID;
   a.cnt = static_cast<int*>(z);
   a.part = reinterpret_cast<float*>(static_cast<uint8_t*>(z) + 4096);
@@ -669,9 +683,10 @@ int launch_m1d(I8Args a, hipStream_t s) {
 }
 
 // ---- chained launches: one persistent workgroup per CU runs the steps in order
+constexpr int kSplitK = 256;
 struct ChainStep {
   I8Args a;
-  int kind;  // bits * 16 + SPLIT
+  int kind;  // bits * 16 + SPLIT, + kSplitK for a split-K step
   int wait;  // 1: the step reads (or overwrites) what earlier steps wrote or read: wait for all of them
 };
 
@@ -698,6 +713,9 @@ __global__ void __launch_bounds__(1024, 1) i8_chain_kernel(const ChainStep* __re
       case 2 * 16 + 1: m1d_body<2, 1, D, MT, true>(st.a, lds, w, target, s); break;
       case 2 * 16 + 2: m1d_body<2, 2, D, MT, true>(st.a, lds, w, target, s); break;
       case 2 * 16 + 4: m1d_body<2, 4, D, MT, true>(st.a, lds, w, target, s); break;
+      case kSplitK + 4 * 16 + 1: m1d_body<4, 1, D, MT, true, true>(st.a, lds, w, target, s); break;
+      case kSplitK + 3 * 16 + 1: m1d_body<3, 1, D, MT, true, true>(st.a, lds, w, target, s); break;
+      case kSplitK + 2 * 16 + 1: m1d_body<2, 1, D, MT, true, true>(st.a, lds, w, target, s); break;
       default: m1d_body<2, 8, D, MT, true>(st.a, lds, w, target, s); break;
     }
     // signal: this workgroup's outputs of steps <= s are stored (each wave waits for its own stores' acknowledgement,
@@ -761,6 +779,10 @@ int m1d_chain_make(int nsteps, const int* bits, const void* const* x, const int*
   ChainStep* h = static_cast<ChainStep*>(calloc((size_t)nsteps, sizeof(ChainStep)));
   if (!h) return AK_OOM;
   size_t smem = 0;
+  // the table, then the split-K steps' scratch (counters and partials, zeroed)
+  const size_t table_bytes = ((size_t)nsteps * sizeof(ChainStep) + 255) & ~(size_t)255;
+  size_t total = table_bytes;
+  std::vector<size_t> zoff((size_t)nsteps, 0);
   for (int i = 0; i < nsteps; ++i) {
     I8Args& a = h[i].a;
     a.segs = segs[i];
@@ -773,17 +795,33 @@ int m1d_chain_make(int nsteps, const int* bits, const void* const* x, const int*
     a.nb = 0;
     a.part = nullptr;
     a.cnt = nullptr;
+    h[i].wait = i > 0 && wait[i] ? 1 : 0;
+    int nr = 0;
+    size_t sks = 0, zb = 0;
+    if (m1d_sk_shape(a, bits[i], mt, &nr, &sks, &zb) && nr * a.P <= num_cus()) {
+      h[i].kind = kSplitK + bits[i] * 16 + 1;
+      a.wg_end[0] = nr * a.P;
+      zoff[(size_t)i] = total;
+      total += (zb + 255) & ~(size_t)255;
+      smem = sks > smem ? sks : smem;
+      continue;
+    }
     M1dShape sh;
     if (plan_m1d(a, bits[i], mt, true, sh)) {
       free(h);
       return AK_INVALID;
     }
     h[i].kind = bits[i] * 16 + sh.split;
-    h[i].wait = i > 0 && wait[i] ? 1 : 0;
     smem = sh.smem > smem ? sh.smem : smem;
   }
   void* d = nullptr;
-  int e = (int)hipMalloc(&d, (size_t)nsteps * sizeof(ChainStep));
+  int e = (int)hipMalloc(&d, total);
+  if (!e && total > table_bytes) e = (int)hipMemset(static_cast<uint8_t*>(d) + table_bytes, 0, total - table_bytes);
+  for (int i = 0; i < nsteps && !e; ++i)
+    if (zoff[(size_t)i]) {
+      h[i].a.cnt = reinterpret_cast<int*>(static_cast<uint8_t*>(d) + zoff[(size_t)i]);
+      h[i].a.part = reinterpret_cast<float*>(static_cast<uint8_t*>(d) + zoff[(size_t)i] + 4096);
+    }
   if (!e) e = (int)hipMemcpy(d, h, (size_t)nsteps * sizeof(ChainStep), hipMemcpyHostToDevice);
   free(h);
   if (e) {

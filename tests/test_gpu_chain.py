@@ -190,25 +190,31 @@ def test_chain_fallback_runs_steps_one_launch_each():
         assert_same(read_outputs(m, flow), oracle_flow(h_host, m, flow), f"fallback group {group} m {m}")
 
 
-def test_chain_at_decode_shapes_matches_launches():
-    """Two 32B-shaped layers (QKV 5120 -> 5120 + 2 x 1024, O, gate_up 5120 -> 55296, down 27648 -> 5120): the chained
-    launch equals one launch per step bit for bit (the oracle is too slow at these sizes to run step by step)."""
+@pytest.mark.parametrize("m", [1, 2])
+def test_chain_at_decode_shapes_matches_launches(m):
+    """Two 32B-shaped layers (QKV 5120 -> 5120 + 2 x 1024, O, gate_up 5120 -> 55296, down 27648 -> 5120; the down
+    steps split k across workgroups): the chained launch equals one launch per step bit for bit, on two runs in a row
+    (the split's counters return to zero); the oracle is too slow at these sizes to run step by step."""
     K = kernels()
     H, KV, INTER = 5120, 1024, 27648
-    h, steps, flow = build(1, [3, 2], H, KV, INTER)
+    h, steps, flow = build(m, [3, 2], H, KV, INTER)
     ch = Chain(steps)
     assert ch.chained
-    h_host = gen_x(4242, H)
+    h_host = gen_x(4242, m * H)
     check(K.ak_memcpy_h2d(h.p, h_host.ctypes.data, h_host.nbytes), "h2d")
     ch.run()
     check(K.ak_synchronize(), "sync")
     assert K.ak_wq_chain_status() == 0
-    got = read_outputs(1, flow)
+    got = read_outputs(m, flow)
+    zero_outputs(flow)
+    ch.run()
+    check(K.ak_synchronize(), "sync")
+    assert_same(read_outputs(m, flow), got, "second chained run")
     zero_outputs(flow)
     for lins, xin, k, ys in flow:
-        gemv(lins[0].bits, xin.p, 1, [l.L for l in lins], k, 128, ys=ys)
+        gemv(lins[0].bits, xin.p, m, [l.L for l in lins], k, 128, ys=ys)
     check(K.ak_synchronize(), "sync")
-    assert_same(got, read_outputs(1, flow), "chain vs launches")
+    assert_same(got, read_outputs(m, flow), "chain vs launches")
     # outputs stay finite and non-trivial through the chain (the data flow carries information)
     last = got[-1][0].astype(np.uint32) << 16
     f = last.view(np.float32)
