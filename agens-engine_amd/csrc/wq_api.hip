@@ -59,11 +59,16 @@ Segs make_segs(int nseg, const void* const* wt, const void* const* st, void* con
   return g;
 }
 
-// the default path for m <= 16 tokens, in launches of at most 8: one or two tokens on the line-load kernel
+// the default path for m <= 16 tokens: 9..16 tokens in one launch of the tokens-in-A-rows kernel where it takes them,
+// else in launches of at most 8: one or two tokens on the line-load kernel
 // (wq_i8m1d.hip) when their activations fit the LDS (measured faster there), otherwise and for 3..8 tokens the
 // tokens-in-A-rows kernel (wq_i8mt.hip; activations beyond the LDS in chunks of stripes), and the any-m kernel
 // (wq_i8.hip) for what neither takes (group 64)
 int run_i8(int bits, const void* x, int m, const Segs& g, int k, int group, hipStream_t s) {
+  if (m > 8) {  // 9..16 tokens in one launch of the tokens-in-A-rows kernel when it takes them
+    const int e = i8_gemv_mt(bits, x, m, g, k, group, s);
+    if (e != AK_INVALID) return e;
+  }
   const int mt = m <= 8 ? m : (m + 1) / 2;
   bool ok = true;
   for (int m0 = 0; m0 < m && ok; m0 += mt) {

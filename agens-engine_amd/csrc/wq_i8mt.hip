@@ -120,14 +120,24 @@ __global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
   int sg = 0;
 #pragma unroll
   for (int i = 1; i < kMaxSegs; ++i) sg += (i < sgs.nseg && (int)blockIdx.x >= a.wg_end[i - 1]) ? 1 : 0;
-  const int nr = SK ? (int)gridDim.x / P : 1, r = SK ? (int)blockIdx.x / P : 0, psk = SK ? (int)blockIdx.x - r * P : 0;
-  const int wg0 = sg ? AK_PICK(sg - 1, a.wg_end) : 0, gs = SK ? nr : AK_PICK(sg, a.wg_end) - wg0;
-  const int w = SK ? r : (int)blockIdx.x - wg0;
+  // (SK: segment i has (wg_end[i] - wg_end[i-1]) / P row ranges; range r of the segment is counter wg0 / P + r, its
+  // partials start after the earlier segments')
+  const int wg0 = sg ? AK_PICK(sg - 1, a.wg_end) : 0, li = (int)blockIdx.x - wg0;
+  const int nr = SK ? (AK_PICK(sg, a.wg_end) - wg0) / P : 1, r = SK ? li / P : 0, psk = SK ? li - r * P : 0;
+  const int gs = SK ? nr : AK_PICK(sg, a.wg_end) - wg0, w = SK ? r : li;
   const int n = AK_PICK(sg, sgs.n), n_b16 = (n + 15) >> 4;
   const int b_lo = (int)((long long)w * n_b16 / gs);
   const int nb = (int)((long long)(w + 1) * n_b16 / gs) - b_lo;
   uint16_t* const yseg = AK_PICK(sg, sgs.y);
   const int ldy = AK_PICK(sg, sgs.ldy);
+  float* spart = a.part;
+  int* scnt = a.cnt;
+  if constexpr (SK) {
+#pragma unroll
+    for (int i = 0; i < kMaxSegs - 1; ++i)
+      if (i < sg) spart += (size_t)P * MP * ((AK_PICK(i, sgs.n) + 15) >> 4) * 16;
+    scnt += wg0 / P + r;
+  }
 
   // chunks of stripes and the groups an activation image holds (the largest chunk's)
   const int nch = CH ? a.nb : 1;
@@ -321,6 +331,7 @@ __global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
       const int g = 4 * cq + s - g0;  // group of the chunk's image
 #pragma unroll
       for (int tg = 0; tg < NT; ++tg) {
+        if constexpr (NT > 2) asm volatile("" ::: "memory");  // one token group's operands live at a time
         const i32x4 mt = meta[(tg * cgs + g) * 4 + h];
         const uint8_t* src = lds + a_lane + g * a_gmul + tg * a_tmul;
         const i32x4 a0 = *reinterpret_cast<const i32x4*>(src);
@@ -357,7 +368,7 @@ __global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
     } else if constexpr (SK) {  // to the range's partials, device-coherent (the range's last workgroup adds them)
 #pragma unroll
       for (int tg = 0; tg < NT; ++tg)
-        __hip_atomic_store(a.part + ((size_t)(ep * MP + 4 * tg + h) * n_b16 + b_lo + eg) * 16 + c, pp[tg],
+        __hip_atomic_store(spart + ((size_t)(ep * MP + 4 * tg + h) * n_b16 + b_lo + eg) * 16 + c, pp[tg],
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     } else if constexpr (SPLIT == 1) {
 #pragma unroll
@@ -425,16 +436,16 @@ __global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
     __syncthreads();
     int* const last = reinterpret_cast<int*>(yl);
     if (tid == 0) {
-      const int old = __hip_atomic_fetch_add(a.cnt + r, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int old = __hip_atomic_fetch_add(scnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       *last = old == P - 1;
-      if (old == P - 1) __hip_atomic_store(a.cnt + r, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next launch
+      if (old == P - 1) __hip_atomic_store(scnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next launch
     }
     __syncthreads();
     if (!*last) return;
     __syncthreads();  // every thread has read the flag before the outputs overwrite it
     for (int i = tid; i < nb * MP * 16; i += 64 * nwv) {
       const int bl = i / (MP * 16), o = i - bl * MP * 16, t = o >> 4;
-      const float* src = a.part + ((size_t)t * n_b16 + b_lo + bl) * 16 + (o & 15);
+      const float* src = spart + ((size_t)t * n_b16 + b_lo + bl) * 16 + (o & 15);
       float y = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       for (int q = 1; q < P; ++q)
         y += __hip_atomic_load(src + (size_t)q * MP * n_b16 * 16, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -463,7 +474,7 @@ size_t mt_block_bytes(int P, int split, int nt) {  // per 16-row block: outputs,
 
 template <int BITS, int SPLIT, int NT, bool CH, bool SK = false>
 void launch_mt_split(const I8Args& a, int grid, size_t smem, hipStream_t s) {
-  constexpr int DEPTH = 2;
+  constexpr int DEPTH = NT > 2 ? 1 : 2;  // items in flight per wave (16 tokens: their accumulators take the registers)
   hipLaunchKernelGGL((i8_mt_kernel<BITS, SPLIT, DEPTH, NT, CH, SK>), dim3(grid), dim3(1024), smem, s, a);
 }
 
@@ -502,7 +513,36 @@ int launch_mt(I8Args a, hipStream_t s) {
     const int nbs = (g.n[i] + 15) / 16, gs = (nbs + per - 1) / per;
     nbmax = (nbs + gs - 1) / gs > nbmax ? (nbs + gs - 1) / gs : nbmax;
   }
+  // split-K across workgroups: P workgroups per row range, each one stripe, partials in the stream's scratch; taken
+  // when the activation image does not fit the LDS, or when the launch has few rows per CU (every workgroup would
+  // convert all of x for at most two 16-row blocks).  Row ranges are shared out over the segments by their blocks.
+  // Without scratch (inside a capture that has not got it yet): the launches below.
   const size_t x_bytes = 256 + (size_t)mt_a_bytes(ngroups, NT) + mt_meta_bytes(ngroups, NT);
+  if (a.P >= 2 && (x_bytes > 140 * 1024 || total <= 2 * cus)) {
+    const int nrt = cus / a.P;
+    int nr[kMaxSegs] = {0, 0, 0, 0}, left = nrt - g.nseg, nbr = 0;
+    size_t part_floats = 0;
+    for (int i = 0; i < g.nseg; ++i) {  // at least one range per segment, the rest by blocks
+      const int nbs = (g.n[i] + 15) / 16;
+      nr[i] = 1 + (int)((long long)left * nbs / total);
+      nbr = (nbs + nr[i] - 1) / nr[i] > nbr ? (nbs + nr[i] - 1) / nr[i] : nbr;
+      part_floats += (size_t)a.P * 4 * NT * nbs * 16;
+    }
+    const int cg = mt_chunk_groups(a.nquad, a.P, a.P);
+    const size_t smem = 256 + (size_t)mt_a_bytes(cg, NT) + mt_meta_bytes(cg, NT) + (size_t)nbr * 4 * NT * 16 * 2 + 16;
+    void* z = nrt >= g.nseg && nrt <= 1024 && smem <= 160 * 1024 ? stream_scratch(s, 4096 + part_floats * 4) : nullptr;
+    if (z) {
+      I8Args b = a;
+      for (int i = 0, e = 0; i < kMaxSegs; ++i) {
+        if (i < g.nseg) e += nr[i] * a.P;
+        b.wg_end[i] = e;
+      }
+      b.cnt = static_cast<int*>(z);
+      b.part = reinterpret_cast<float*>(static_cast<uint8_t*>(z) + 4096);
+      launch_mt_split<BITS, 1, NT, false, true>(b, b.wg_end[g.nseg - 1], smem, s);
+      return (int)hipGetLastError();
+    }
+  }
   if (x_bytes <= 140 * 1024) {
     // the whole activation image fits: tasks per block = fewest quad rounds for the busiest wave, a task's overhead
     // counted as about one quad
@@ -531,21 +571,6 @@ int launch_mt(I8Args a, hipStream_t s) {
       return (int)hipGetLastError();
     }
   }
-  // split-K across workgroups (one segment): P workgroups per row range, each one stripe, partials in the stream's
-  // scratch; without scratch (inside a capture that has not got it yet) the chunked launch below
-  if (g.nseg == 1 && a.P >= 2) {
-    const int cus = num_cus(), nr = cus / a.P > 0 ? cus / a.P : 1, nbs = (g.n[0] + 15) / 16;
-    const int nbr = (nbs + nr - 1) / nr, cg = mt_chunk_groups(a.nquad, a.P, a.P);
-    const size_t smem = 256 + (size_t)mt_a_bytes(cg, NT) + mt_meta_bytes(cg, NT) + (size_t)nbr * 4 * NT * 16 * 2 + 16;
-    const size_t cnt_bytes = 4096, part_bytes = (size_t)a.P * 4 * NT * nbs * 16 * 4;
-    void* z = nr <= 1024 && smem <= 160 * 1024 ? stream_scratch(s, cnt_bytes + part_bytes) : nullptr;
-    if (z) {
-      a.cnt = static_cast<int*>(z);
-      a.part = reinterpret_cast<float*>(static_cast<uint8_t*>(z) + cnt_bytes);
-      launch_mt_split<BITS, 1, NT, false, true>(a, nr * a.P, smem, s);
-      return (int)hipGetLastError();
-    }
-  }
   // chunked: the fewest chunks of stripes whose image, with every block's stripe partials, fits the LDS
   const size_t blk = (size_t)4 * NT * 16 * 2 + (size_t)a.P * 4 * NT * 16 * 4;
   for (int nch = 2; nch <= a.P; ++nch) {
@@ -561,11 +586,11 @@ int launch_mt(I8Args a, hipStream_t s) {
 
 }  // namespace
 
-// 1..8 tokens (4 or 8 in the kernel), 16-row blocks (the last one padded); activations beyond the LDS in chunks of
-// stripes.  Returns AK_INVALID if the shape does not suit the kernel (group 64, a segment beyond 2 GB, a chunk of
+// 1..16 tokens (4, 8 or 16 in the kernel), 16-row blocks (the last one padded); activations beyond the LDS: split-K
+// across workgroups or chunks of stripes.  Returns AK_INVALID if the shape does not suit the kernel (group 64, a segment beyond 2 GB, a chunk of
 // one stripe beyond the LDS): the caller falls back.
 int i8_gemv_mt(int bits, const void* x, int m, const Segs& g, int k, int group, hipStream_t s) {
-  if (group != kG || m < 1 || m > 8) return AK_INVALID;
+  if (group != kG || m < 1 || m > 16) return AK_INVALID;
 #ifdef AK_NO_MT
   return AK_INVALID;
 #endif
@@ -580,7 +605,7 @@ int i8_gemv_mt(int bits, const void* x, int m, const Segs& g, int k, int group, 
   a.nb = 0;
   a.part = nullptr;
   a.cnt = nullptr;
-  const int nt = m <= 4 ? 1 : 2;
+  const int nt = m <= 4 ? 1 : m <= 8 ? 2 : 4;
   switch (bits * 10 + nt) {
     case 41: return launch_mt<4, 1>(a, s);
     case 31: return launch_mt<3, 1>(a, s);
@@ -588,6 +613,9 @@ int i8_gemv_mt(int bits, const void* x, int m, const Segs& g, int k, int group, 
     case 42: return launch_mt<4, 2>(a, s);
     case 32: return launch_mt<3, 2>(a, s);
     case 22: return launch_mt<2, 2>(a, s);
+    case 44: return launch_mt<4, 4>(a, s);
+    case 34: return launch_mt<3, 4>(a, s);
+    case 24: return launch_mt<2, 4>(a, s);
     default: return AK_INVALID;
   }
 }

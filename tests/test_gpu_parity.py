@@ -301,3 +301,28 @@ def test_long_k_small_m(bits, m):
     for j in (0, m - 1):
         one = y_of(gemv(bits, X.addr(j * k * 2), 1, [A], k, g)[0], 1, 900)[0]
         assert (one == y1[j]).all()
+
+
+@pytest.mark.parametrize("bits", [4, 3, 2])
+@pytest.mark.parametrize("m", [3, 8, 16])
+@pytest.mark.parametrize("k", [2048, 27648])
+def test_multi_segment_small_m_oracle(bits, m, k):
+    """Unequal segments (a QKV-like 640 / 128 / 128 split) at 3..16 tokens, with an ldy stride on the first: every
+    segment equals the oracle (the launch splits k across workgroups, row ranges shared out over the segments)."""
+    g = 128
+    ns = (640, 128, 128)
+    parts = [make_linear(1300 + 10 * bits + i, ni, k, g, bits) for i, ni in enumerate(ns)]
+    x = gen_x(1350 + m, m * k)
+    X = Dev.of(x)
+    ld0 = 700
+    ys = [Dev(m * ld0 * 2), Dev(m * ns[1] * 2), Dev(m * ns[2] * 2)]
+    for _ in range(2):  # twice: the split's counters return to zero
+        gemv(bits, X, m, parts, k, g, ldy=[ld0, ns[1], ns[2]], ys=[y.p for y in ys])
+        for i, (L, y) in enumerate(zip(parts, ys)):
+            wt, st = L.host_kt()
+            got = y_of(y, m, L.n, ld0 if i == 0 else None)[:, :L.n]
+            rows = (0, 64) if k > 8192 else None
+            want = ora_fast(bits, x, m, wt, st, L.n, k, g, rows=rows)
+            if rows:
+                got, want = got[:, :64], want[:, :64]
+            assert (got == want).all(), f"segment {i}"
