@@ -488,6 +488,11 @@ int mt_chunk_groups(int nquad, int P, int nch) {
   return cg;
 }
 
+// split-K for activations beyond the LDS up to this many 16-row blocks per CU (above it the partials' traffic costs
+// more than the chunked launch's repeated passes)
+#ifndef AK_MT_SK_BLOCKS
+#define AK_MT_SK_BLOCKS 8
+#endif
 template <int BITS, int NT>
 int launch_mt(I8Args a, hipStream_t s) {
   const Segs& g = a.segs;
@@ -514,11 +519,11 @@ int launch_mt(I8Args a, hipStream_t s) {
     nbmax = (nbs + gs - 1) / gs > nbmax ? (nbs + gs - 1) / gs : nbmax;
   }
   // split-K across workgroups: P workgroups per row range, each one stripe, partials in the stream's scratch; taken
-  // when the activation image does not fit the LDS, or when the launch has few rows per CU (every workgroup would
-  // convert all of x for at most two 16-row blocks).  Row ranges are shared out over the segments by their blocks.
+  // when the launch has few rows per CU (every workgroup would convert all of x for at most two 16-row blocks), or
+  // when the activation image does not fit the LDS and there are not many rows per CU.  Row ranges are shared out over the segments by their blocks.
   // Without scratch (inside a capture that has not got it yet): the launches below.
   const size_t x_bytes = 256 + (size_t)mt_a_bytes(ngroups, NT) + mt_meta_bytes(ngroups, NT);
-  if (a.P >= 2 && (x_bytes > 140 * 1024 || total <= 2 * cus)) {
+  if (a.P >= 2 && (total <= 2 * cus || (x_bytes > 140 * 1024 && total <= AK_MT_SK_BLOCKS * cus))) {
     const int nrt = cus / a.P;
     int nr[kMaxSegs] = {0, 0, 0, 0}, left = nrt - g.nseg, nbr = 0;
     size_t part_floats = 0;
