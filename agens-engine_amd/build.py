@@ -19,7 +19,8 @@ LIB = os.path.join(HERE, "libagens_kernels.so")
 BENCH_LIB = os.path.join(HERE, "libagens_bench.so")
 HOST = os.path.join(HERE, "host")
 HOST_LIB = os.path.join(HERE, "libagens_linear.so")
-SOURCES = ["ak_runtime.hip", "wq_layout.hip", "wq_exact.hip", "wq_i8.hip", "wq_i8m1d.hip", "wq_i8mt.hip", "wq_api.hip"]
+SOURCES = ["ak_runtime.hip", "wq_layout.hip", "wq_exact.hip", "wq_i8.hip", "wq_i8m1d.hip", "wq_i8mt.hip", "wq_api.hip",
+           "wq_prefill.hip"]
 
 
 def hipcc():
@@ -56,7 +57,9 @@ def build(jobs=None, verbose=True):
     with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as ex:
         objs = list(ex.map(_compile, SOURCES))
     tmp = LIB + ".tmp"
-    cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", "-Wl,--no-undefined", "-o", tmp] + objs
+    rocm_lib = os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "lib")
+    cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", "-Wl,--no-undefined", "-o", tmp] + objs + [
+        "-L" + rocm_lib, "-lrocblas", "-Wl,-rpath," + rocm_lib]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError("link failed:\n" + r.stdout + r.stderr)

@@ -1,6 +1,9 @@
 // Host side of the quantized-linear path (see agens_linear.h).
 #include "agens_linear.h"
 
+#include <algorithm>
+#include <mutex>
+
 #include "agens_kernels.h"
 
 namespace agens {
@@ -94,8 +97,53 @@ KtPair wq_upload_kt(int bits, const std::vector<uint8_t>& packed, const std::vec
   return out;
 }
 
+namespace {
+size_t g_tile_bytes = (size_t)64 << 20;  // bound of the dequantized tile (the reference's S.wdq / g_w4_tile_bytes)
+std::mutex g_wdq_mu;
+void* g_wdq = nullptr;  // the process's dequantization scratch (grown on demand, held for the process)
+size_t g_wdq_bytes = 0;
+
+// output rows per prefill tile (m1_model.cu:1822-1826): multiples of 256 within the tile bound, at least 256
+int tile_rows(int k, int n) {
+  const long r = (long)(g_tile_bytes / ((size_t)k * 2)) & ~255L;
+  return (int)std::max(256L, std::min<long>(r, n));
+}
+}  // namespace
+
+void set_prefill_tile_bytes(size_t bytes) { g_tile_bytes = bytes; }
+
 int linear(const QuantLinear& t, const void* x, void* y, int m, int n, int k, int bf16w, void* stream) {
-  if (t.n != n || t.k != k || m < 1 || m > 128 || t.np < 1 || t.np > 2) return 1;
+  if (t.n != n || t.k != k || m < 1 || t.np < 1 || t.np > 2) return 1;
+  if (m > 128) {
+    // prefill (m1_model.cu:1876-1897): dequantize a tile of output rows at a time into the bounded scratch and GEMM
+    // that column tile of y (tiles by output row whatever the parts)
+    const int tn = tile_rows(k, n);
+    std::lock_guard<std::mutex> lock(g_wdq_mu);
+    const size_t need = (size_t)std::min(tn, n) * k * 2;
+    if (g_wdq_bytes < need) {
+      if (g_wdq) ak_free(g_wdq);
+      g_wdq = nullptr;
+      g_wdq_bytes = 0;
+      if (const int e = ak_malloc(&g_wdq, need)) return e;
+      g_wdq_bytes = need;
+    }
+    uint16_t* const wdq = static_cast<uint16_t*>(g_wdq);
+    for (int n0 = 0; n0 < n; n0 += tn) {
+      const int nt = std::min(tn, n - n0);
+      for (int j = 0; j < t.np; ++j) {
+        const QuantPart& q = t.p[j];
+        const int a0 = std::max(n0, q.r0), a1 = std::min(n0 + nt, q.r0 + q.n);
+        if (a0 < a1)
+          if (const int e = ak_wq_dequant_kt_rows(q.bits, q.wt, q.st, wdq + (size_t)(a0 - n0) * k, q.n, k, q.group,
+                                                  a0 - q.r0, a1 - a0, stream))
+            return e;
+      }
+      if (tn >= n) return ak_bf16_linear_f32reduce(x, wdq, y, m, n, k, stream);
+      if (const int e = ak_bf16_linear_f32reduce_ld(x, wdq, static_cast<uint16_t*>(y) + n0, m, nt, k, n, stream))
+        return e;
+    }
+    return 0;
+  }
   for (int j = 0; j < t.np; ++j) {
     const QuantPart& q = t.p[j];
     void* yp = static_cast<uint16_t*>(y) + q.r0;

@@ -68,10 +68,13 @@ struct QuantLinear {
   QuantPart p[2];
 };
 
-// Decode / verify linear (m1_model.cu:1857-1875): y[m][n] = x[m][k] W^T, one ak_wq_gemv_kt_multi per part with
-// ldy = n.  Returns 0 or an error code; 1 for a shape mismatch or m beyond the batched GEMV (m > 128: the prefill
-// dequantize + GEMM route is not part of this path).
+// The model's linear (m1_model.cu:1857-1900): y[m][n] = x[m][k] W^T.  Up to 128 tokens one ak_wq_gemv_kt_multi per
+// part with ldy = n; above, the prefill route: tiles of output rows dequantized (ak_wq_dequant_kt_rows) into a bounded
+// scratch of the process and multiplied by ak_bf16_linear_f32reduce(_ld).  Returns 0 or an error code; 1 for a shape
+// mismatch.  The prefill route allocates its scratch on first use (not under stream capture) and is not re-entrant.
 int linear(const QuantLinear& t, const void* x, void* y, int m, int n, int k, int bf16w, void* stream);
+// bytes of one dequantized prefill tile (default 64 MB; the reference's tile bound, m1_model.cu:1822-1826)
+void set_prefill_tile_bytes(size_t bytes);
 
 // Linears sharing x (m1_model.cu:1904-1937): one launch per (bits, group) class of single-part linears when m == 1
 // (outputs bit-identical to separate GEMVs), otherwise one linear() each.

@@ -110,6 +110,15 @@ int ak_w4_dequant_kt_rows(const void* wt, const void* st, void* w, int n, int k,
 int ak_w3_dequant_kt_rows(const void* wt, const void* st, void* w, int n, int k, int group, int r0, int nr,
                           void* stream);          /* agens_kernels.h:247-248 */
 
+/* ---------------------------------------------------------------------------------------------- prefill GEMM
+ * y[m][ldy] = x[m][k] W^T, bf16 x and W [n][k] (the dequantized rows of ak_wq_dequant_kt_rows), fp32 accumulation,
+ * bf16 y; the model's linear() takes this route above 128 tokens.  A library GEMM (rocBLAS gemm_ex), not a kernel of
+ * this library; its accumulation order is the library's (results within fp32-accumulation tolerance of the oracle). */
+int ak_bf16_linear_f32reduce(const void* x, const void* w, void* y, int m, int n, int k,
+                             void* stream);       /* agens_kernels.h:55, bf16_linear.cu:82-92 */
+int ak_bf16_linear_f32reduce_ld(const void* x, const void* w, void* y, int m, int n, int k, int ldy,
+                                void* stream);    /* agens_kernels.h:56, bf16_linear.cu:68-80 */
+
 /* ---------------------------------------------------------------------------------------------- chained GEMV steps
  * No single counterpart in the reference: it replaces a run of ak_wq_gemv_kt_multi launches joined by programmatic
  * dependent launch edges in a captured graph (reference: ak_graph_pdl, kernels/src/runtime.cu:198-230, and the

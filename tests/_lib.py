@@ -293,6 +293,8 @@ def kernels():
             "ak_w4_dequant_kt": (i, [vp, vp, vp, i, i, i, vp]),
             "ak_w4_dequant_kt_rows": (i, [vp, vp, vp, i, i, i, i, i, vp]),
             "ak_w3_dequant_kt_rows": (i, [vp, vp, vp, i, i, i, i, i, vp]),
+            "ak_bf16_linear_f32reduce": (i, [vp, vp, vp, i, i, i, vp]),
+            "ak_bf16_linear_f32reduce_ld": (i, [vp, vp, vp, i, i, i, i, vp]),
             "ak_wq_chain_create": (i, [ctypes.POINTER(WqStep), i, ctypes.POINTER(c_void_p)]),
             "ak_wq_chain_run": (i, [vp, vp]),
             "ak_wq_chain_chained": (i, [vp]),

@@ -1,6 +1,7 @@
 // GPU test of the C++ host side (agens-engine_amd/host/agens_linear.h): uploads, linear() and linear_shared() against
 // direct C-ABI launches, bit for bit, plus the error behaviour of the reference's host code (lib.rs:176-213,
 // m1_model.cu:1857-1937).  Run by tests/test_host_linear.py; prints "host linear: OK" on success.
+#include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <vector>
@@ -88,6 +89,43 @@ int main() {
         same = same && hy[(size_t)j * 160 + r] == (r < 96 ? h0[(size_t)j * 96 + r] : h1[(size_t)j * 64 + r - 96]);
     EXPECT(same, "linear parts == direct launches");
     EXPECT(linear(gu, x.ptr(), y.ptr(), m, 161, k, 0, nullptr) == 1, "shape mismatch -> 1");
+  }
+  // ---- prefill (m > 128): dequantized tiles x GEMM, against fp64 products of the dequantized weights (tolerance of an
+  // fp32-accumulated GEMM: 1 bf16 ulp of the result + 1e-5 of sum |x * w|), one tile and tiles of 256 rows
+  {
+    const int m = 200, n = 160;
+    std::vector<uint16_t> hx((size_t)m * k);
+    for (auto& v : hx) v = f2bf(-1.f + 2.f * (rnd() >> 8) / 16777216.f);
+    DeviceBuffer x = upload(hx.data(), hx.size() * 2), y((size_t)m * n * 2), wd((size_t)n * k * 2);
+    check(ak_wq_dequant_kt_rows(3, a.first.ptr(), a.second.ptr(), wd.ptr(), 96, k, g, 0, 96, nullptr), "dequant W3");
+    check(ak_wq_dequant_kt_rows(4, b.first.ptr(), b.second.ptr(), static_cast<uint16_t*>(wd.ptr()) + (size_t)96 * k, 64,
+                                k, g, 0, 64, nullptr),
+          "dequant W4");
+    const auto hw = get(wd.ptr(), (size_t)n * k);
+    auto bf = [](uint16_t b) {
+      uint32_t u = (uint32_t)b << 16;
+      float f;
+      std::memcpy(&f, &u, 4);
+      return (double)f;
+    };
+    for (size_t tile : {(size_t)64 << 20, (size_t)256 * k * 2}) {
+      set_prefill_tile_bytes(tile);
+      EXPECT(linear(gu, x.ptr(), y.ptr(), m, n, k, 0, nullptr) == 0, "prefill linear");
+      const auto hy = get(y.ptr(), (size_t)m * n);
+      int bad = 0;
+      for (int i = 0; i < m; ++i)
+        for (int r = 0; r < n; ++r) {
+          double ref = 0, mag = 0;
+          for (int c = 0; c < k; ++c) {
+            const double p = bf(hx[(size_t)i * k + c]) * bf(hw[(size_t)r * k + c]);
+            ref += p, mag += std::fabs(p);
+          }
+          const double ulp = std::ldexp(1.0, (int)std::floor(std::log2(std::fabs(ref) + 1e-30)) - 7);
+          bad += std::fabs(bf(hy[(size_t)i * n + r]) - ref) > ulp + 1e-5 * mag;
+        }
+      EXPECT(bad == 0, "prefill linear == dequantized weights x x");
+    }
+    set_prefill_tile_bytes((size_t)64 << 20);
   }
   // ---- linear_shared: three single-part linears of mixed bits sharing x (two classes: W3 and W4)
   std::vector<uint8_t> pa, sa, pb, sb, pc, sc;
