@@ -11,8 +11,12 @@
  *     other values are hipError_t codes;
  *   - `stream` is a hipStream_t (NULL = the default stream); launches are asynchronous and stream-ordered;
  *   - bf16 tensors are passed as void* (raw 16-bit patterns), the int4 container as int32_t words;
- *   - the caller owns every buffer it passes; the GEMV entry points allocate nothing (no scratch memory) and never
- *     synchronize, so they can be captured in a hipGraph.
+ *   - the caller owns every buffer it passes.  The GEMV entry points own scratch only for split-K launches (long k, or
+ *     few rows per CU, at more than two tokens or long k): per (device, stream), allocated zero-filled on the first
+ *     such call outside a stream capture (that call synchronizes the device once), grown when a larger launch needs
+ *     it, held until the process ends -- as the reference's split-K scratch (w4_gemv.cu:2096-2118).  Inside a capture
+ *     they never allocate or synchronize: without scratch they take a launch that needs none (same results), so they
+ *     can be captured in a hipGraph.
  */
 #pragma once
 #include <stddef.h>
