@@ -118,9 +118,15 @@ static_assert(kMaxSegs == 4, "segment selects cover four segments");
 // device-coherent (sc1, L2 write-through) stores and acknowledged; a step that reads earlier steps' outputs first
 // issues its first weight loads (constant data), then waits until every workgroup's flag has reached the step, then
 // reads its activations with device-coherent loads.  No L2 write-back or invalidate is needed on either side.
-constexpr int kChainMaxWg = 1024, kChainFlagStride = 16;
+// Flags are packed 4 bytes apart (AK_CHAIN_DENSE, the default): a poll reads 16 flags per 64-byte line, one 16-byte
+// load per lane, so a poll round of the whole GPU is 256 x 16 line requests instead of 256 x 256 (each one a miss
+// of the L2, since the loads are device-coherent).
+#ifndef AK_CHAIN_DENSE
+#define AK_CHAIN_DENSE 1
+#endif
+constexpr int kChainMaxWg = 1024, kChainFlagStride = AK_CHAIN_DENSE ? 1 : 16;
 constexpr long long kChainSpinTicks = 20000000;  // 0.2 s of the 100 MHz wall clock: a bounded wait, then an error
-__device__ uint32_t g_chain_flags[kChainMaxWg * kChainFlagStride];
+__device__ __attribute__((aligned(256))) uint32_t g_chain_flags[kChainMaxWg * kChainFlagStride];
 __device__ uint32_t g_chain_err;
 
 // per-step phase timestamps of a chained launch, in probe builds only (-DAK_CHAIN_PROBE; product builds compile
@@ -153,10 +159,20 @@ __device__ __forceinline__ void chain_poll(uint32_t target) {
   const long long t0 = wall_clock64();
   for (;;) {
     bool ok = true;
-    for (int j = lane; j < nwg; j += 64) {
-      const uint32_t v = __hip_atomic_load(g_chain_flags + j * kChainFlagStride, __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-      ok = ok && (int)(v - target) >= 0;
+    if constexpr (AK_CHAIN_DENSE) {
+      const __amdgpu_buffer_rsrc_t rf =
+          __builtin_amdgcn_make_buffer_rsrc(g_chain_flags, (short)0, kChainMaxWg * 4, kRsrcWord3);
+      for (int j = 4 * lane; j < nwg; j += 256) {
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rf, j * 4, 0, kSc1);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ok = ok && (j + i >= nwg || (int)(v[i] - target) >= 0);
+      }
+    } else {
+      for (int j = lane; j < nwg; j += 64) {
+        const uint32_t v = __hip_atomic_load(g_chain_flags + j * kChainFlagStride, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+        ok = ok && (int)(v - target) >= 0;
+      }
     }
     if (__all(ok)) break;
     if (wall_clock64() - t0 > kChainSpinTicks) {
@@ -213,8 +229,9 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
   // the quads the activation image holds: [q0, q0 + nqs) (SK: stripe psk; else all)
   const int q0 = SK ? stripe_begin(psk, nquad, P, 2) : 0;
   const int nqs = SK ? stripe_begin(psk + 1, nquad, P, 2) - q0 : nquad;
-  const int b_lo = (int)((long long)w * n_b4 / gs);
-  const int nb = (int)((long long)(w + 1) * n_b4 / gs) - b_lo;
+  // 32-bit divisions (w < 1024 workgroups, < 2^21 blocks): a 64-bit one is a long instruction sequence on the GPU
+  const int b_lo = (int)((unsigned)w * (unsigned)n_b4 / (unsigned)gs);
+  const int nb = (int)((unsigned)(w + 1) * (unsigned)n_b4 / (unsigned)gs) - b_lo;
   uint16_t* const yseg = AK_PICK(sg, sgs.y);
   const int ldy = AK_PICK(sg, sgs.ldy);
 

@@ -126,8 +126,9 @@ __global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
   const int nr = SK ? (AK_PICK(sg, a.wg_end) - wg0) / P : 1, r = SK ? li / P : 0, psk = SK ? li - r * P : 0;
   const int gs = SK ? nr : AK_PICK(sg, a.wg_end) - wg0, w = SK ? r : li;
   const int n = AK_PICK(sg, sgs.n), n_b16 = (n + 15) >> 4;
-  const int b_lo = (int)((long long)w * n_b16 / gs);
-  const int nb = (int)((long long)(w + 1) * n_b16 / gs) - b_lo;
+  // 32-bit divisions (w < 1024 workgroups, < 2^21 blocks): a 64-bit one is a long instruction sequence on the GPU
+  const int b_lo = (int)((unsigned)w * (unsigned)n_b16 / (unsigned)gs);
+  const int nb = (int)((unsigned)(w + 1) * (unsigned)n_b16 / (unsigned)gs) - b_lo;
   uint16_t* const yseg = AK_PICK(sg, sgs.y);
   const int ldy = AK_PICK(sg, sgs.ldy);
   float* spart = a.part;
