@@ -20,8 +20,18 @@ struct I8Args {
 // Stripes are contiguous runs of whole 1024-input tiles: with nt = nquad / qpt tiles, P = min(8, nt) stripes and stripe
 // p = tiles [p * nt / P, (p + 1) * nt / P), i.e. quads [qpt * (p * nt / P), qpt * ((p + 1) * nt / P)).
 __host__ __device__ inline int stripe_count(int nquad, int qpt) { return nquad / qpt < 8 ? nquad / qpt : 8; }
-// first quad of stripe p
-__host__ __device__ inline int stripe_begin(int p, int nquad, int P, int qpt) { return qpt * (p * (nquad / qpt) / P); }
+// x / d for 0 <= x < 2^23 and 1 <= d <= 8 by a multiply with ceil(2^32 / d) (exact in that range: the error term
+// x (M d - 2^32) / (d 2^32) < 2^-9 stays below the distance 1 / d of x / d to the next integer); a runtime 32-bit
+// division is a long instruction sequence on the GPU, and the scalar unit running it is shared by the CU's waves
+__host__ __device__ inline int div_upto8(int x, int d) {
+  const unsigned m = d == 2 ? 2147483649u : d == 3 ? 1431655766u : d == 4 ? 1073741825u : d == 5 ? 858993460u
+                   : d == 6 ? 715827883u : d == 7 ? 613566757u : 536870913u;
+  return d == 1 ? x : (int)(((unsigned long long)(unsigned)x * m) >> 32);
+}
+// first quad of stripe p (p <= P <= 8, fewer than 2^20 tiles)
+__host__ __device__ inline int stripe_begin(int p, int nquad, int P, int qpt) {
+  return qpt * div_upto8(p * (nquad / qpt), P);
+}
 
 namespace {
 

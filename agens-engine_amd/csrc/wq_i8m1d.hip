@@ -205,7 +205,7 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
   constexpr int REC = 128 * BITS;  // one row's tile record
   const int P = a.P, nquad = a.nquad, k = a.k, mm = a.m;  // mm <= MT tokens (the others are zero, not written)
   const int ntile = nquad >> 1;
-  const int nwv = blockDim.x >> 6;
+  const int nwv = CHAIN ? 16 : blockDim.x >> 6;  // a chained launch has 16 waves
   int tid = threadIdx.x;
   // chained: an opaque thread index per step, so that nothing lane-dependent is hoisted out of the step loop (the
   // hoisted values would stay live across every step's item loop)
