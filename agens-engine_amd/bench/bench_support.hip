@@ -53,6 +53,16 @@ __global__ void gen_x_kernel(uint64_t seed, size_t count, float xs, uint16_t* x)
     x[i] = to_bf16(normal(seed, i) * xs);
 }
 
+__global__ void gen_i8_kernel(uint64_t seed, size_t words, uint32_t* q) {  // uniform int8 bytes
+  for (size_t w = blockIdx.x * (size_t)blockDim.x + threadIdx.x; w < words; w += (size_t)gridDim.x * blockDim.x)
+    q[w] = mix(seed, w) ^ (mix(seed + 1, w) << 16);
+}
+
+__global__ void gen_f32_kernel(uint64_t seed, size_t count, float sa, float sb, float* s) {  // |N(0,1)| sa + sb
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < count; i += (size_t)gridDim.x * blockDim.x)
+    s[i] = fabsf(normal(seed, i)) * sa + sb;
+}
+
 __global__ void read_kernel(const uint4* __restrict__ p, size_t n16, uint32_t* out) {
   uint32_t acc = 0;
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n16; i += (size_t)gridDim.x * blockDim.x) {
@@ -106,6 +116,63 @@ int agb_gen_x(uint64_t seed, size_t count, float xs, void* x, void* stream) {
   hipLaunchKernelGGL(gen_x_kernel, dim3(grid_for(count)), dim3(256), 0, (hipStream_t)stream, seed, count, xs,
                      (uint16_t*)x);
   return (int)hipGetLastError();
+}
+
+int agb_gen_i8(uint64_t seed, size_t bytes, void* q, void* stream) {  // bytes % 4 == 0
+  hipLaunchKernelGGL(gen_i8_kernel, dim3(grid_for(bytes / 4)), dim3(256), 0, (hipStream_t)stream, seed, bytes / 4,
+                     (uint32_t*)q);
+  return (int)hipGetLastError();
+}
+
+int agb_gen_f32(uint64_t seed, size_t count, float sa, float sb, void* s, void* stream) {
+  hipLaunchKernelGGL(gen_f32_kernel, dim3(grid_for(count)), dim3(256), 0, (hipStream_t)stream, seed, count, sa, sb,
+                     (float*)s);
+  return (int)hipGetLastError();
+}
+
+// ak_i8_gemv over `ncopies` weight copies in turn (w + c * n * k, scale + c * n), `steps` launches captured in one
+// hipGraph after `warmup` eager ones; *ms = the mean time per launch (HIP events on the launching stream).
+int agb_time_i8_gemv(const void* x, const void* w, const void* scale, void* y, int m, int n, int k, int ncopies,
+                     int warmup, int steps, float* ms) {
+  hipStream_t s;
+  int e = (int)hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+  if (e) return e;
+  auto one = [&](int i) {
+    const int c = i % ncopies;
+    return ak_i8_gemv(x, (const int8_t*)w + (size_t)c * n * k, (const float*)scale + (size_t)c * n, y, m, n, k, n, s);
+  };
+  for (int i = 0; i < warmup && !e; ++i) e = one(i);
+  hipGraph_t g = nullptr;
+  hipGraphExec_t ge = nullptr;
+  bool cap = false;
+  if (!e) {
+    e = (int)hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+    cap = !e;
+  }
+  for (int i = 0; i < steps && !e; ++i) e = one(i);
+  if (cap) {
+    const int e2 = (int)hipStreamEndCapture(s, &g);
+    if (!e) e = e2;
+  }
+  if (!e) e = (int)hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+  if (!e) e = (int)hipGraphLaunch(ge, s);  // first replay untimed
+  hipEvent_t a, b;
+  hipEventCreate(&a);
+  hipEventCreate(&b);
+  if (!e) e = (int)hipEventRecord(a, s);
+  if (!e) e = (int)hipGraphLaunch(ge, s);
+  if (!e) e = (int)hipEventRecord(b, s);
+  if (!e) e = (int)hipEventSynchronize(b);
+  float t = 0.f;
+  if (!e) e = (int)hipEventElapsedTime(&t, a, b);
+  *ms = t / steps;
+  hipEventDestroy(a);
+  hipEventDestroy(b);
+  if (ge) hipGraphExecDestroy(ge);
+  if (g) hipGraphDestroy(g);
+  hipStreamSynchronize(s);
+  hipStreamDestroy(s);
+  return e;
 }
 
 static int launch_one(const AgbLaunch& L, hipStream_t s) {

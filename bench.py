@@ -10,7 +10,7 @@ reference's int4 container and repacked by ak_wq_repack_kt; inputs are resident 
 
 Effective bytes per launch = packed weights + bf16 scales + bf16 x + bf16 y (the algorithmic bytes).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--m 1] [--config sweep|0|1|2|3] [--no-cpu] [--eager]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--m 1] [--config sweep|0|1|2|3|i8] [--no-cpu] [--eager]
 """
 import argparse
 import ctypes
@@ -60,6 +60,9 @@ def load_libs():
         ("agb_run_chain", i, [ctypes.POINTER(AgbLaunch), i, i, i, i, ctypes.POINTER(ctypes.c_float),
                               ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int)]),
         ("agb_read_bw", i, [sz, i, ctypes.POINTER(ctypes.c_float)]),
+        ("agb_gen_i8", i, [ctypes.c_uint64, sz, vp, vp]),
+        ("agb_gen_f32", i, [ctypes.c_uint64, sz, ctypes.c_float, ctypes.c_float, vp, vp]),
+        ("agb_time_i8_gemv", i, [vp, vp, vp, vp, i, i, i, i, i, i, ctypes.POINTER(ctypes.c_float)]),
     ]:
         f = getattr(B, name)
         f.restype, f.argtypes = res, args
@@ -369,6 +372,33 @@ def run_single(args, K, B):
     return lines
 
 
+def run_i8(args, K, B):
+    """The INT8 LM head GEMV (ak_i8_gemv; reference i8_gemv.cu): 152064 x 5120 int8 weights with fp32 row scales,
+    M = 1, 4, 16 tokens; two weight copies in turn (each 778 MB, beyond the 256 MB cache)."""
+    ctx = Ctx(K, B)
+    n, k, copies = 152064, 5120, 2
+    w = ctx.alloc(copies * n * k)
+    sc = ctx.alloc(copies * n * 4)
+    ctx.check(B.agb_gen_i8(SEED + 31, copies * n * k, w, None), "gen i8")
+    ctx.check(B.agb_gen_f32(SEED + 32, copies * n, 0.02 * 3 / 127, 1e-6, sc, None), "gen scales")
+    lines = []
+    for m in ([args.m] if args.m != 1 else [1, 4, 16]):
+        x = ctx.alloc(m * k * 2)
+        y = ctx.alloc(m * n * 2)
+        ctx.check(B.agb_gen_x(SEED + 33, m * k, 1.0, x, None), "gen x")
+        t = ctypes.c_float()
+        ctx.check(B.agb_time_i8_gemv(x, w, sc, y, m, n, k, copies, args.warmup, max(args.steps, 10),
+                                     ctypes.byref(t)), "i8 gemv")
+        us = t.value * 1e3
+        by = n * k + n * 4 + m * k * 2 + m * n * 2
+        lines.append({"config": "i8_lm_head", "n": n, "k": k, "m": m, "us": round(us, 2),
+                      "GBps": round(by / (us * 1e-6) / 1e9, 1),
+                      "pct_of_peak": round(100 * by / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 2), "bytes": by,
+                      "copies": copies, "graph": True})
+    ctx.free_all()
+    return lines
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -401,6 +431,9 @@ def main():
             raise RuntimeError("calibration copy failed")
     if args.config == "sweep":
         print(json.dumps(run_sweep(args, K, B)), flush=True)
+    elif args.config == "i8":
+        for line in run_i8(args, K, B):
+            print(json.dumps(line), flush=True)
     else:
         args.config = int(args.config)
         for line in run_single(args, K, B):

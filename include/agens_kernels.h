@@ -123,6 +123,14 @@ int ak_bf16_linear_f32reduce(const void* x, const void* w, void* y, int m, int n
 int ak_bf16_linear_f32reduce_ld(const void* x, const void* w, void* y, int m, int n, int k, int ldy,
                                 void* stream);    /* agens_kernels.h:56, bf16_linear.cu:68-80 */
 
+/* ---------------------------------------------------------------------------------------------- INT8 LM head GEMV
+ * W8A16: y[j][o] (row stride ldy) = bf16(scale[o] * sum_i x[j][i] * q[o][i]); q int8 [n][k] row-major, scale fp32 [n]
+ * (per-row symmetric), x bf16 [m][k]; 1 <= m <= 16, k % 16 == 0 (else 1).  The reference's fp32 order (32 chunk-strided
+ * partials of 16-input fma chains, xor butterfly), kept exactly: bit-identical to the reference, and row j of an
+ * m-token call is bit-identical to the 1-token call. */
+int ak_i8_gemv(const void* x, const void* w, const void* scale, void* y, int m, int n, int k, int ldy,
+               void* stream);                     /* agens_kernels.h:264, i8_gemv.cu:72-88 */
+
 /* ---------------------------------------------------------------------------------------------- chained GEMV steps
  * No single counterpart in the reference: it replaces a run of ak_wq_gemv_kt_multi launches joined by programmatic
  * dependent launch edges in a captured graph (reference: ak_graph_pdl, kernels/src/runtime.cu:198-230, and the

@@ -415,3 +415,32 @@ void ora_gen_scales(uint64_t seed, size_t count, float sa, float sb, uint16_t* s
 void ora_gen_x(uint64_t seed, size_t count, float xs, uint16_t* x) {
   for (size_t i = 0; i < count; ++i) x[i] = ora_f2bf((float)(normal_at(seed, i) * xs));
 }
+
+/* ------------------------------------------------------------------------------------------------ adjacent GEMVs */
+/* kernels/src/i8_gemv.cu:28-70: the warp of row o (32 lanes), lane l over chunks l, l + 32, ...; per chunk a 16-input
+ * fmaf chain from 0 (dot4 x 4, inputs in order), added to the lane's sum; then the xor butterfly and the row scale */
+void ora_i8_gemv(const uint16_t* x, const int8_t* q, const float* scale, uint16_t* y, int m, int n, int k, int ldy) {
+  const int chunks = k / 16;
+  for (int o = 0; o < n; ++o) {
+    const int8_t* w = q + (size_t)o * k;
+    for (int j = 0; j < m; ++j) {
+      const uint16_t* xr = x + (size_t)j * k;
+      float v[32];
+      for (int l = 0; l < 32; ++l) {
+        float acc = 0.f;
+        for (int c = l; c < chunks; c += 32) {
+          float s = 0.f;
+          for (int e = 0; e < 16; ++e) s = fmaf(ora_bf2f(xr[16 * c + e]), (float)w[16 * c + e], s);
+          acc += s;
+        }
+        v[l] = acc;
+      }
+      for (int d = 16; d > 0; d >>= 1) {
+        float t[32];
+        for (int l = 0; l < 32; ++l) t[l] = v[l] + v[l ^ d];
+        memcpy(v, t, sizeof(v));
+      }
+      y[(size_t)j * ldy + o] = ora_f2bf(v[0] * scale[o]);
+    }
+  }
+}

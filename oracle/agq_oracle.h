@@ -37,6 +37,13 @@ void ora_kt_chunk(int bits, const uint8_t* wt, size_t rec, int lane, uint32_t ou
 int ora_dequant_kt_rows(int bits, const uint8_t* wt, const uint16_t* st, uint16_t* w, int n, int k, int group, int r0,
                         int nr);
 
+/* ---- adjacent GEMVs */
+/* INT8 LM head (W8A16): kernels/src/i8_gemv.cu:28-70 (dot4, i8_gemv_kernel).  q int8 [n][k], scale fp32 [n], k % 16 == 0;
+ * y[j * ldy + o] = bf16_rn(v * scale[o]), v = xor butterfly (distance 16, 8, 4, 2, 1: v[l] + v[l ^ d]) of 32 partials,
+ * partial l = sum over the 16-input chunks c = l, l + 32, ... (in that order) of s, s = fmaf(x_e, q_e, s) from 0 over
+ * the chunk's inputs e = 0..15. */
+void ora_i8_gemv(const uint16_t* x, const int8_t* q, const float* scale, uint16_t* y, int m, int n, int k, int ldy);
+
 /* ---- GEMV references.  x bf16 [m][k] (row stride k); y written per token j at y + j * ldy. */
 /* reference.rs:53-71 (w4::gemv) generalised to group G: per group ga += x*q in fp32, then acc += ga * s (no fma).
  * Reads the int4 container.  nthreads > 1 splits output rows statically over POSIX threads (same bits). */

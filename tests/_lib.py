@@ -65,6 +65,7 @@ def oracle():
             "ora_gen_container": (V, [c_uint64, c_int, c_int, c_int, c_int, c_void_p]),
             "ora_gen_scales": (V, [c_uint64, c_size_t, c_float, c_float, c_void_p]),
             "ora_gen_x": (V, [c_uint64, c_size_t, c_float, c_void_p]),
+            "ora_i8_gemv": (V, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int]),
         }
         for name, (res, args) in sigs.items():
             f = getattr(L, name)
@@ -295,6 +296,7 @@ def kernels():
             "ak_w3_dequant_kt_rows": (i, [vp, vp, vp, i, i, i, i, i, vp]),
             "ak_bf16_linear_f32reduce": (i, [vp, vp, vp, i, i, i, vp]),
             "ak_bf16_linear_f32reduce_ld": (i, [vp, vp, vp, i, i, i, i, vp]),
+            "ak_i8_gemv": (i, [vp, vp, vp, vp, i, i, i, i, vp]),
             "ak_wq_chain_create": (i, [ctypes.POINTER(WqStep), i, ctypes.POINTER(c_void_p)]),
             "ak_wq_chain_run": (i, [vp, vp]),
             "ak_wq_chain_chained": (i, [vp]),

@@ -55,6 +55,11 @@ def test_invalid_arguments_return_1_without_a_gpu(K):
     assert K.ak_wq_dequant_kt_rows(4, nul, nul, nul, 16, 1024, 128, 10, 10, None) == 1  # r0 + nr > n
     assert K.ak_w4g128_gemv_kt_variant(33, nul, nul, nul, nul, 16, 1024, None) == 1
     assert K.ak_w4g128_gemv_kt_tune(3, 1, 8, 0, nul, nul, nul, nul, 16, 1024, None) == 1
+    # i8_gemv.cu:74: m outside 1..16 or k % 16 -> 1
+    one = ctypes.c_void_p(16)
+    assert K.ak_i8_gemv(one, one, one, one, 0, 16, 1024, 16, None) == 1
+    assert K.ak_i8_gemv(one, one, one, one, 17, 16, 1024, 16, None) == 1
+    assert K.ak_i8_gemv(one, one, one, one, 1, 16, 1000, 16, None) == 1
 
 
 def test_switches(K):

@@ -242,3 +242,65 @@ def test_oracle_wq_equals_w4(bits):
     _, wtb, stb = ora_repack(bits, packed, scales, n, k, group)
     assert (ora_fast(4, x, m, wt4, st4, n, k, group) == ora_fast(bits, x, m, wtb, stb, n, k, group)).all()
     assert (ora_exact(4, x, m, wt4, st4, n, k, group) == ora_exact(bits, x, m, wtb, stb, n, k, group)).all()
+
+
+# ------------------------------------------------------------------------------------------------ INT8 LM head GEMV
+def ora_i8(x, q, scale, m, n, k, ldy=None):
+    ldy = ldy or n
+    y = np.zeros(m * ldy, dtype=np.uint16)
+    oracle().ora_i8_gemv(ptr(x), ptr(q), ptr(scale), ptr(y), m, n, k, ldy)
+    return y
+
+
+def test_i8_gemv_exact_integer_products():
+    """Small-integer activations: every product and partial sum is an exact fp32 integer, so any summation order gives
+    the exact dot product; y = bf16(fp32(S) * scale) pins the indexing (chunks, inputs, tokens, rows)."""
+    rng = np.random.default_rng(5)
+    m, n, k = 3, 9, 16 * 65  # 65 chunks: lanes 0 gets three, others two
+    xi = rng.integers(-4, 5, size=(m, k))
+    q = rng.integers(-128, 128, size=(n, k)).astype(np.int8)
+    scale = (rng.random(n) * 0.01 + 1e-3).astype(np.float32)
+    x = f2bf_array(xi.astype(np.float32).ravel())
+    y = ora_i8(x, q, scale, m, n, k).reshape(m, n)
+    S = xi.astype(np.int64) @ q.astype(np.int64).T  # exact
+    want = f2bf_array((S.astype(np.float32) * scale[None, :]).ravel()).reshape(m, n)
+    assert np.array_equal(y, want)
+
+
+def test_i8_gemv_summation_order_known_answers():
+    """Hand-computed values where the reference's order (i8_gemv.cu:44-70) differs from a plain left-to-right sum:
+    lane l's partial takes chunks l, l + 32, ..., each chunk's fma chain starts from 0, and the 32 partials meet in an
+    xor butterfly.  k = 64 chunks, q = 1 where x is set, scale 1."""
+    k, n, m = 16 * 64, 1, 1
+    q = np.ones((n, k), dtype=np.int8)
+    scale = np.ones(n, dtype=np.float32)
+
+    def run(vals):
+        xf = np.zeros(k, dtype=np.float32)
+        for i, v in vals.items():
+            xf[i] = v
+        return bf2f_array(ora_i8(f2bf_array(xf), q, scale, m, n, k))[0]
+
+    # chunks 0 (lane 0): 2^24, 1 (lane 1): 1, 2 (lane 2): -2^24, 3 (lane 3): 1.  Butterfly distance 2 pairs lanes
+    # 0 + 2 = 0 and 1 + 3 = 2, distance 1 gives 2; left to right gives ((2^24 + 1) - 2^24) + 1 = 1
+    assert run({0: 2.0 ** 24, 16: 1.0, 32: -(2.0 ** 24), 48: 1.0}) == 2.0
+    # lane 0: chunk 0 = 2^24, chunk 32 = 1 + 1 (its own chain from 0: 2) -> 2^24 + 2; lane 2: chunk 2 = -2^24.
+    # Result 2; one fma chain carried across chunks would give 2^24 + 1 + 1 = 2^24 and then 0
+    assert run({0: 2.0 ** 24, 16 * 32: 1.0, 16 * 32 + 1: 1.0, 32: -(2.0 ** 24)}) == 2.0
+    # within a chunk the chain is sequential: 2^24, 1, -2^24 in inputs 0..2 of chunk 0: fma(1, 1, 2^24) = 2^24,
+    # then 0 (a pairwise sum of the chunk would keep the 1)
+    assert run({0: 2.0 ** 24, 1: 1.0, 2: -(2.0 ** 24)}) == 0.0
+
+
+def test_i8_gemv_within_fp64_bound():
+    rng = np.random.default_rng(7)
+    m, n, k = 2, 33, 5120
+    x = f2bf_array(rng.standard_normal(m * k).astype(np.float32))
+    q = rng.integers(-127, 128, size=(n, k)).astype(np.int8)
+    scale = (rng.random(n) * 0.02 + 1e-4).astype(np.float32)
+    y = bf2f_array(ora_i8(x, q, scale, m, n, k)).reshape(m, n).astype(np.float64)
+    xf = bf2f_array(x).reshape(m, k).astype(np.float64)
+    ref = (xf @ q.astype(np.float64).T) * scale[None, :]
+    mag = (np.abs(xf) @ np.abs(q.astype(np.float64)).T) * scale[None, :]
+    # bf16 output rounding (2^-9 relative) plus fp32 summation error (k * 2^-24 of sum |x q|)
+    assert np.all(np.abs(y - ref) <= np.abs(ref) * 2.0 ** -8 + mag * k * 2.0 ** -24)
