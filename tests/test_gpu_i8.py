@@ -34,7 +34,7 @@ def run(x, q, scale, m, n, k, ldy=None, fill=0x7FC1):
     return Y.get(np.uint16, m * ldy)
 
 
-@pytest.mark.parametrize("m,n,k", [(1, 64, 5120), (1, 301, 1040), (3, 77, 16), (5, 130, 4096), (8, 19, 2064),
+@pytest.mark.parametrize("m,n,k", [(1, 64, 5120), (1, 301, 1040), (1, 40, 16400), (3, 77, 16), (5, 130, 4096), (8, 19, 2064),
                                    (9, 40, 5120), (16, 33, 3072)])
 def test_matches_oracle_bit_exact(m, n, k):
     x, q, scale = data(11 + m, m, n, k)
