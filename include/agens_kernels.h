@@ -131,6 +131,17 @@ int ak_bf16_linear_f32reduce_ld(const void* x, const void* w, void* y, int m, in
 int ak_i8_gemv(const void* x, const void* w, const void* scale, void* y, int m, int n, int k, int ldy,
                void* stream);                     /* agens_kernels.h:264, i8_gemv.cu:72-88 */
 
+/* ---------------------------------------------------------------------------------------------- batch-invariant bf16 GEMV
+ * y[t][r] (row stride ldy; n for ak_bf16_gemv_bi) = bf16(sum_i x[t][i] W[r][i] (+ bias[r])); W bf16 [n][k] row-major,
+ * x bf16 [m][k], bias bf16 [n] or NULL; 1 <= m <= 128, k % 32 == 0 (else 1).  fp32 accumulation (MFMA), the bias added
+ * in fp32 before the one bf16 rounding, and a summation order that does not depend on m: row t of an m-token call is
+ * bit-identical to the 1-token call.  The reference's bits come from its tensor-core MMA's internal accumulation, so
+ * results agree with the reference within fp32-accumulation tolerance, not bit for bit. */
+int ak_bf16_gemv_bi(const void* x, const void* w, const void* bias, void* y, int m, int n, int k,
+                    void* stream);                /* agens_kernels.h:88, bi_gemv.cu:270-273 */
+int ak_bf16_gemv_bi_ld(const void* x, const void* w, const void* bias, void* y, int m, int n, int k, long ldy,
+                       void* stream);             /* agens_kernels.h:89, bi_gemv.cu:274-356 */
+
 /* ---------------------------------------------------------------------------------------------- chained GEMV steps
  * No single counterpart in the reference: it replaces a run of ak_wq_gemv_kt_multi launches joined by programmatic
  * dependent launch edges in a captured graph (reference: ak_graph_pdl, kernels/src/runtime.cu:198-230, and the

@@ -60,6 +60,10 @@ def test_invalid_arguments_return_1_without_a_gpu(K):
     assert K.ak_i8_gemv(one, one, one, one, 0, 16, 1024, 16, None) == 1
     assert K.ak_i8_gemv(one, one, one, one, 17, 16, 1024, 16, None) == 1
     assert K.ak_i8_gemv(one, one, one, one, 1, 16, 1000, 16, None) == 1
+    # bi_gemv.cu:276: m outside 1..128 or k % 32 -> 1
+    assert K.ak_bf16_gemv_bi(one, one, None, one, 0, 16, 1024, None) == 1
+    assert K.ak_bf16_gemv_bi(one, one, None, one, 129, 16, 1024, None) == 1
+    assert K.ak_bf16_gemv_bi_ld(one, one, None, one, 1, 16, 1040, 16, None) == 1
 
 
 def test_switches(K):
