@@ -142,6 +142,17 @@ int ak_bf16_gemv_bi(const void* x, const void* w, const void* bias, void* y, int
 int ak_bf16_gemv_bi_ld(const void* x, const void* w, const void* bias, void* y, int m, int n, int k, long ldy,
                        void* stream);             /* agens_kernels.h:89, bi_gemv.cu:274-356 */
 
+/* ---------------------------------------------------------------------------------------------- SiLU(gate) * up
+ * out[t][i] = bf16(g / (1 + exp(-g)) * u) for g = gate_up[t][i], u = gate_up[t][inter + i] (the merged gate_up output
+ * [tokens][2 inter] -> [tokens][inter]); inter % 8 == 0 (else 1).  _part: one tensor-parallel share [gate share | up
+ * share] (np each) -> the full row of inter, the share's products at [lo, lo + np) and zeros elsewhere.  The
+ * reference compiles the expression with CUDA's fast-math exp and division; here exp is the device library's expf and
+ * the division an fp32 division: results within one bf16 unit in the last place of the reference's, not bit for bit. */
+int ak_silu_mul(const void* gate_up, void* out, int tokens, int inter,
+                void* stream);                    /* agens_kernels.h:110, silu_mul.cu:66-72 */
+int ak_silu_mul_part(const void* gate_up_part, void* out, int inter, int lo, int np,
+                     void* stream);               /* agens_kernels.h:113, silu_mul.cu:58-64 */
+
 /* ---------------------------------------------------------------------------------------------- chained GEMV steps
  * No single counterpart in the reference: it replaces a run of ak_wq_gemv_kt_multi launches joined by programmatic
  * dependent launch edges in a captured graph (reference: ak_graph_pdl, kernels/src/runtime.cu:198-230, and the

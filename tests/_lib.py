@@ -298,6 +298,8 @@ def kernels():
             "ak_bf16_linear_f32reduce_ld": (i, [vp, vp, vp, i, i, i, i, vp]),
             "ak_i8_gemv": (i, [vp, vp, vp, vp, i, i, i, i, vp]),
             "ak_bf16_gemv_bi": (i, [vp, vp, vp, vp, i, i, i, vp]),
+            "ak_silu_mul": (i, [vp, vp, i, i, vp]),
+            "ak_silu_mul_part": (i, [vp, vp, i, i, i, vp]),
             "ak_bf16_gemv_bi_ld": (i, [vp, vp, vp, vp, i, i, i, ctypes.c_long, vp]),
             "ak_wq_chain_create": (i, [ctypes.POINTER(WqStep), i, ctypes.POINTER(c_void_p)]),
             "ak_wq_chain_run": (i, [vp, vp]),
