@@ -13,14 +13,6 @@
 namespace agq {
 namespace {
 
-__device__ __forceinline__ uint4 silu_mul8(const uint4 g, const uint4 u) {
-  const uint32_t gw[4] = {g.x, g.y, g.z, g.w}, uw[4] = {u.x, u.y, u.z, u.w};
-  uint32_t o[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) o[i] = silu_mul_pair(gw[i], uw[i]);
-  return make_uint4(o[0], o[1], o[2], o[3]);
-}
-
 // tokens x inter / 8 vectors of 8 outputs
 __global__ void silu_mul_kernel(const uint4* __restrict__ in, uint4* __restrict__ out, unsigned nv, unsigned total) {
   const unsigned tid = blockIdx.x * blockDim.x + threadIdx.x;

@@ -17,10 +17,10 @@ namespace agq {
 int exact_gemv(int bits, const void* x, int m, const Segs& g, int k, int group, int bf16w, hipStream_t s);
 int exact_ct_gemv(const void* x, const int32_t* packed, const void* scales, void* y, int n, int k, hipStream_t s);
 int i8_gemv(int bits, const void* x, int m, const Segs& g, int k, int group, hipStream_t s);
-int i8_gemv_m1(int bits, const void* x, int m, const Segs& g, int k, int group, hipStream_t s);
-int i8_gemv_mt(int bits, const void* x, int m, const Segs& g, int k, int group, hipStream_t s);
+int i8_gemv_m1(int bits, const void* x, int m, const Segs& g, int k, int group, hipStream_t s, int act = 0);
+int i8_gemv_mt(int bits, const void* x, int m, const Segs& g, int k, int group, hipStream_t s, int act = 0);
 int m1d_chain_make(int nsteps, const int* bits, const void* const* x, const int* m, const int* k, const Segs* segs,
-                   const int* wait, void** table, int* mt_out, size_t* smem_out);
+                   const int* wait, const int* act, void** table, int* mt_out, size_t* smem_out);
 int m1d_chain_launch(const void* table, int nsteps, int mt, size_t smem, hipStream_t s);
 int m1d_chain_error(int* err);
 
@@ -63,22 +63,24 @@ Segs make_segs(int nseg, const void* const* wt, const void* const* st, void* con
 // else in launches of at most 8: one or two tokens on the line-load kernel
 // (wq_i8m1d.hip) when their activations fit the LDS (measured faster there), otherwise and for 3..8 tokens the
 // tokens-in-A-rows kernel (wq_i8mt.hip; activations beyond the LDS in chunks of stripes), and the any-m kernel
-// (wq_i8.hip) for what neither takes (group 64)
-int run_i8(int bits, const void* x, int m, const Segs& g, int k, int group, hipStream_t s) {
+// (wq_i8.hip) for what neither takes (group 64).  act = 1 (x = gate_up [m][2k], activations SiLU(gate) * up): the
+// any-m kernel does not take it (AK_INVALID).
+int run_i8(int bits, const void* x, int m, const Segs& g, int k, int group, hipStream_t s, int act = 0) {
   if (m > 8) {  // 9..16 tokens in one launch of the tokens-in-A-rows kernel when it takes them
-    const int e = i8_gemv_mt(bits, x, m, g, k, group, s);
+    const int e = i8_gemv_mt(bits, x, m, g, k, group, s, act);
     if (e != AK_INVALID) return e;
   }
+  const size_t xk = act ? 2 * (size_t)k : (size_t)k;  // x's token stride
   const int mt = m <= 8 ? m : (m + 1) / 2;
   bool ok = true;
   for (int m0 = 0; m0 < m && ok; m0 += mt) {
     const int mm = m - m0 < mt ? m - m0 : mt;
     Segs gg = g;
     for (int i = 0; i < g.nseg; ++i) gg.y[i] = g.y[i] + (size_t)m0 * g.ldy[i];
-    const void* xx = static_cast<const uint16_t*>(x) + (size_t)m0 * k;
-    int e = mm <= 2 ? i8_gemv_m1(bits, xx, mm, gg, k, group, s) : AK_INVALID;
-    if (e == AK_INVALID) e = i8_gemv_mt(bits, xx, mm, gg, k, group, s);
-    if (e == AK_INVALID) e = i8_gemv_m1(bits, xx, mm, gg, k, group, s);
+    const void* xx = static_cast<const uint16_t*>(x) + (size_t)m0 * xk;
+    int e = mm <= 2 ? i8_gemv_m1(bits, xx, mm, gg, k, group, s, act) : AK_INVALID;
+    if (e == AK_INVALID) e = i8_gemv_mt(bits, xx, mm, gg, k, group, s, act);
+    if (e == AK_INVALID) e = i8_gemv_m1(bits, xx, mm, gg, k, group, s, act);
     if (e == AK_INVALID && m0 == 0) {
       ok = false;
     } else if (e) {
@@ -86,24 +88,26 @@ int run_i8(int bits, const void* x, int m, const Segs& g, int k, int group, hipS
     }
   }
   if (ok) return 0;
+  if (act) return AK_INVALID;
   return i8_gemv(bits, x, m, g, k, group, s);
 }
 
 int gemv(int bits, const void* x, int m, int nseg, const void* const* wt, const void* const* st, void* const* y,
-         const int* n, const int* ldy, int k, int group, int bf16w, bool force_default, hipStream_t s) {
+         const int* n, const int* ldy, int k, int group, int bf16w, bool force_default, hipStream_t s, int act = 0) {
   if (!group_ok(k, group) || nseg < 1 || nseg > kMaxSegs || m < 1 || m > 128) return AK_INVALID;
   if (bits < 2 || bits > 4 || !x || !wt || !st || !y || !n) return AK_INVALID;
   for (int i = 0; i < nseg; ++i)
     if (n[i] < 1 || !wt[i] || !st[i] || !y[i] || (ldy && ldy[i] < n[i])) return AK_INVALID;
   const bool exact = bf16w || (!force_default && exact_mode());
+  if (act && exact) return AK_INVALID;  // the fused activation is in the default path's kernels only
   for (int m0 = 0; m0 < m; m0 += kMaxTokensPerLaunch) {
     const int mm = m - m0 < kMaxTokensPerLaunch ? m - m0 : kMaxTokensPerLaunch;
     void* yy[kMaxSegs];
     for (int i = 0; i < nseg; ++i)
       yy[i] = static_cast<uint16_t*>(y[i]) + (size_t)m0 * (ldy ? ldy[i] : n[i]);
-    const void* xx = static_cast<const uint16_t*>(x) + (size_t)m0 * k;
+    const void* xx = static_cast<const uint16_t*>(x) + (size_t)m0 * (act ? 2 * (size_t)k : (size_t)k);
     const int e = exact ? exact_gemv(bits, xx, mm, make_segs(nseg, wt, st, yy, n, ldy, 1), k, group, bf16w, s)
-                        : run_i8(bits, xx, mm, make_segs(nseg, wt, st, yy, n, ldy, 16), k, group, s);
+                        : run_i8(bits, xx, mm, make_segs(nseg, wt, st, yy, n, ldy, 16), k, group, s, act);
     if (e) return e;
   }
   return 0;
@@ -120,7 +124,7 @@ struct Chain {
 
 int step_args_ok(const ak_wq_step& st) {
   if (!group_ok(st.k, st.group) || st.nseg < 1 || st.nseg > kMaxSegs || st.m < 1 || st.m > 128) return 0;
-  if (st.bits < 2 || st.bits > 4 || !st.x) return 0;
+  if (st.bits < 2 || st.bits > 4 || !st.x || st.act < 0 || st.act > 1) return 0;
   for (int i = 0; i < st.nseg; ++i)
     if (st.n[i] < 1 || !st.wt[i] || !st.st[i] || !st.y[i] || (st.ldy[i] && st.ldy[i] < st.n[i])) return 0;
   return 1;
@@ -129,7 +133,7 @@ int step_args_ok(const ak_wq_step& st) {
 int run_step(const ak_wq_step& st, hipStream_t s) {
   int ldy[kMaxSegs];
   for (int i = 0; i < st.nseg; ++i) ldy[i] = st.ldy[i] ? st.ldy[i] : st.n[i];
-  return gemv(st.bits, st.x, st.m, st.nseg, st.wt, st.st, st.y, st.n, ldy, st.k, st.group, st.bf16w, false, s);
+  return gemv(st.bits, st.x, st.m, st.nseg, st.wt, st.st, st.y, st.n, ldy, st.k, st.group, st.bf16w, false, s, st.act);
 }
 
 }  // namespace
@@ -142,6 +146,12 @@ extern "C" {
 int ak_wq_gemv_kt_multi(int bits, const void* x, int m, int nseg, const void* const* wt, const void* const* st,
                         void* const* y, const int* n, const int* ldy, int k, int group, int bf16w, void* stream) {
   return gemv(bits, x, m, nseg, wt, st, y, n, ldy, k, group, bf16w, false, static_cast<hipStream_t>(stream));
+}
+
+int ak_wq_gemv_kt_silu(int bits, const void* gate_up, int m, const void* wt, const void* st, void* y, int n, int ldy,
+                       int inter, int group, void* stream) {
+  const int ld = ldy ? ldy : n;
+  return gemv(bits, gate_up, m, 1, &wt, &st, &y, &n, &ld, inter, group, 0, false, static_cast<hipStream_t>(stream), 1);
 }
 
 int ak_w4_gemv_kt(const void* x, const void* wt, const void* st, void* y, int n, int k, int group, int bf16w,
@@ -235,20 +245,20 @@ int ak_wq_chain_create(const ak_wq_step* steps, int nsteps, void** chain) {
   for (int i = 0; i < nsteps && chainable; ++i)
     chainable = steps[i].bf16w == 0 && steps[i].group == 128 && steps[i].m <= 2;
   if (chainable) {
-    int* ib = static_cast<int*>(malloc(sizeof(int) * 4 * (size_t)nsteps));
+    int* ib = static_cast<int*>(malloc(sizeof(int) * 5 * (size_t)nsteps));
     const void** xs = static_cast<const void**>(malloc(sizeof(void*) * (size_t)nsteps));
     Segs* sg = static_cast<Segs*>(malloc(sizeof(Segs) * (size_t)nsteps));
     int e = ib && xs && sg ? 0 : AK_OOM;
     if (!e) {
-      int *bits = ib, *m = ib + nsteps, *k = ib + 2 * nsteps, *wait = ib + 3 * nsteps;
+      int *bits = ib, *m = ib + nsteps, *k = ib + 2 * nsteps, *wait = ib + 3 * nsteps, *act = ib + 4 * nsteps;
       for (int i = 0; i < nsteps; ++i) {
         const ak_wq_step& st = steps[i];
         int ldy[kMaxSegs];
         for (int j = 0; j < st.nseg; ++j) ldy[j] = st.ldy[j] ? st.ldy[j] : st.n[j];
-        bits[i] = st.bits, m[i] = st.m, k[i] = st.k, wait[i] = !st.independent, xs[i] = st.x;
+        bits[i] = st.bits, m[i] = st.m, k[i] = st.k, wait[i] = !st.independent, xs[i] = st.x, act[i] = st.act;
         sg[i] = make_segs(st.nseg, st.wt, st.st, st.y, st.n, ldy, 16);
       }
-      e = m1d_chain_make(nsteps, bits, xs, m, k, sg, wait, &c->table, &c->mt, &c->smem);
+      e = m1d_chain_make(nsteps, bits, xs, m, k, sg, wait, act, &c->table, &c->mt, &c->smem);
     }
     free(ib);
     free(xs);

@@ -2,6 +2,7 @@
 // The numerics they implement are described at the top of wq_i8.hip.
 #pragma once
 #include "wq_common.h"
+#include "wq_silu.h"
 
 namespace agq {
 
@@ -15,6 +16,7 @@ struct I8Args {
   int wg_end[4];  // m = 1 kernel: workgroups of segments 0..i (each workgroup serves one segment)
   float* part;    // split-K launches: stripe partials [P][tokens][rows] and, at cnt, one counter per row range
   int* cnt;
+  int act = 0;    // 1: x is the merged gate_up [m][2k] and the activations are SiLU(gate) * up (wq_silu.h)
 };
 
 // Stripes are contiguous runs of whole 1024-input tiles: with nt = nquad / qpt tiles, P = min(8, nt) stripes and stripe

@@ -197,7 +197,7 @@ __device__ __forceinline__ void lds_barrier() {
 // SK (split-K across workgroups, one segment): workgroup (r, p) computes stripe p of the rows of range r, converting
 // only that stripe's activations; it writes its stripe partials with device-coherent stores, and the last of the
 // range's P workgroups (device-scope counter) adds them in stripe order and writes y.
-template <int BITS, int SPLIT, int DEPTH, int MT, bool CHAIN, bool SK = false>
+template <int BITS, int SPLIT, int DEPTH, int MT, bool CHAIN, bool SK = false, bool ACT = false>
 __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wait, uint32_t target, int ps = 0) {
   static_assert(!SK || SPLIT == 1, "a split launch gives every wave whole stripes of its blocks");
   AK_PROBE(ps, 0);
@@ -257,8 +257,11 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
   const int u0 = wave * UPW + lane / LPU;
   const int npass = (units + ustride - 1) / ustride;
   uint4 xv[XB];
+  // ACT: x is gate_up [mm][2k], the activation SiLU(gate) * up of the two halves (the same value as ak_silu_mul's)
+  constexpr bool act = ACT;
+  const int xk = act ? 2 * k : k;  // x's token stride
   const __amdgpu_buffer_rsrc_t rx =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.x), (short)0, mm * k * 2, kRsrcWord3);
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.x), (short)0, mm * xk * 2, kRsrcWord3);
   (void)rx;
   auto xload = [&](int pass0) {
 #pragma unroll
@@ -268,12 +271,19 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
       const bool ok = u < units && t < mm && kk < k;
       xv[b] = make_uint4(0u, 0u, 0u, 0u);
       if (pass0 + b < npass) {
+        const int xo = ok ? t * xk + kk : 0;
         if constexpr (CHAIN) {  // device-coherent: x may be an earlier step's output, written by another XCD
-          const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? (int)(((size_t)t * k + kk) * 2) : 0, 0, kSc1);
-          xv[b] = ok ? make_uint4(v[0], v[1], v[2], v[3]) : make_uint4(0u, 0u, 0u, 0u);
+          const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rx, xo * 2, 0, kSc1);
+          uint4 g = make_uint4(v[0], v[1], v[2], v[3]);
+          if (act) {
+            const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rx, (xo + k) * 2, 0, kSc1);
+            g = silu_mul8(g, make_uint4(w[0], w[1], w[2], w[3]));
+          }
+          xv[b] = ok ? g : make_uint4(0u, 0u, 0u, 0u);
         } else {
-          const uint4 v = *reinterpret_cast<const uint4*>(a.x + (ok ? (size_t)t * k + kk : 0));
-          xv[b] = ok ? v : make_uint4(0u, 0u, 0u, 0u);
+          uint4 g = *reinterpret_cast<const uint4*>(a.x + xo);
+          if (act) g = silu_mul8(g, *reinterpret_cast<const uint4*>(a.x + xo + k));
+          xv[b] = ok ? g : make_uint4(0u, 0u, 0u, 0u);
         }
       }
     }
@@ -563,11 +573,11 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
   }
 }
 
-template <int BITS, int SPLIT, int DEPTH, int MT, bool SK = false>
+template <int BITS, int SPLIT, int DEPTH, int MT, bool SK = false, bool ACT = false>
 __global__ void __launch_bounds__(1024, 1) i8_m1d_kernel(const I8Args a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   AK_M1_WG_BEGIN();
-  m1d_body<BITS, SPLIT, DEPTH, MT, false, SK>(a, lds, false, 0u);
+  m1d_body<BITS, SPLIT, DEPTH, MT, false, SK, ACT>(a, lds, false, 0u);
   AK_M1_WG_END();
 }
 
@@ -639,9 +649,10 @@ int plan_m1d(I8Args& a, int bits, int mt, bool chain, M1dShape& sh) {
 
 constexpr int m1d_depth(int mt) { return mt <= 2 ? AK_M1_TILES : 1; }  // items in flight per wave
 
-template <int BITS, int SPLIT, int MT>
+template <int BITS, int SPLIT, int MT, bool ACT>
 void launch_split(const I8Args& a, int grid, int nwv, size_t smem, hipStream_t s) {
-  hipLaunchKernelGGL((i8_m1d_kernel<BITS, SPLIT, m1d_depth(MT), MT>), dim3(grid), dim3(64 * nwv), smem, s, a);
+  hipLaunchKernelGGL((i8_m1d_kernel<BITS, SPLIT, m1d_depth(MT), MT, false, ACT>), dim3(grid), dim3(64 * nwv), smem, s,
+                     a);
 }
 
 // split-K across workgroups (one segment, 8 stripes, k of at least AK_M1_SK_QUADS quads): P workgroups per row range,
@@ -670,7 +681,7 @@ bool m1d_sk_shape(const I8Args& a, int bits, int mt, int* nr_out, size_t* smem_o
   return true;
 }
 
-template <int BITS, int MT>
+template <int BITS, int MT, bool ACT>
 int launch_m1d_sk(I8Args a, hipStream_t s) {
   if constexpr (MT > 2) return AK_INVALID;  // 3..8 tokens: the tokens-in-A-rows kernel has its own split
   int nr = 0;
@@ -681,29 +692,34 @@ int launch_m1d_sk(I8Args a, hipStream_t s) {
   a.cnt = static_cast<int*>(z);
   a.part = reinterpret_cast<float*>(static_cast<uint8_t*>(z) + 4096);
   a.wg_end[0] = nr * a.P;
-  hipLaunchKernelGGL((i8_m1d_kernel<BITS, 1, m1d_depth(MT), MT, true>), dim3(nr * a.P), dim3(1024), smem, s, a);
+  hipLaunchKernelGGL((i8_m1d_kernel<BITS, 1, m1d_depth(MT), MT, true, ACT>), dim3(nr * a.P), dim3(1024), smem, s, a);
+  return (int)hipGetLastError();
+}
+
+template <int BITS, int MT, bool ACT>
+int launch_m1d_act(I8Args a, hipStream_t s) {
+  if (launch_m1d_sk<BITS, MT, ACT>(a, s) != AK_INVALID) return (int)hipGetLastError();
+  M1dShape sh;
+  if (plan_m1d(a, BITS, MT, false, sh)) return AK_INVALID;
+  switch (sh.split) {
+    case 1: launch_split<BITS, 1, MT, ACT>(a, sh.grid, sh.nwv, sh.smem, s); break;
+    case 2: launch_split<BITS, 2, MT, ACT>(a, sh.grid, sh.nwv, sh.smem, s); break;
+    case 4: launch_split<BITS, 4, MT, ACT>(a, sh.grid, sh.nwv, sh.smem, s); break;
+    default: launch_split<BITS, 8, MT, ACT>(a, sh.grid, sh.nwv, sh.smem, s); break;
+  }
   return (int)hipGetLastError();
 }
 
 template <int BITS, int MT>
 int launch_m1d(I8Args a, hipStream_t s) {
-  if (launch_m1d_sk<BITS, MT>(a, s) != AK_INVALID) return (int)hipGetLastError();
-  M1dShape sh;
-  if (plan_m1d(a, BITS, MT, false, sh)) return AK_INVALID;
-  switch (sh.split) {
-    case 1: launch_split<BITS, 1, MT>(a, sh.grid, sh.nwv, sh.smem, s); break;
-    case 2: launch_split<BITS, 2, MT>(a, sh.grid, sh.nwv, sh.smem, s); break;
-    case 4: launch_split<BITS, 4, MT>(a, sh.grid, sh.nwv, sh.smem, s); break;
-    default: launch_split<BITS, 8, MT>(a, sh.grid, sh.nwv, sh.smem, s); break;
-  }
-  return (int)hipGetLastError();
+  return a.act ? launch_m1d_act<BITS, MT, true>(a, s) : launch_m1d_act<BITS, MT, false>(a, s);
 }
 
 // ---- chained launches: one persistent workgroup per CU runs the steps in order
-constexpr int kSplitK = 256;
+constexpr int kSplitK = 256, kAct = 512;
 struct ChainStep {
   I8Args a;
-  int kind;  // bits * 16 + SPLIT, + kSplitK for a split-K step
+  int kind;  // bits * 16 + SPLIT, + kSplitK for a split-K step, + kAct for a split-K step with SiLU(gate) * up
   int wait;  // 1: the step reads (or overwrites) what earlier steps wrote or read: wait for all of them
 };
 
@@ -733,6 +749,9 @@ __global__ void __launch_bounds__(1024, 1) i8_chain_kernel(const ChainStep* __re
       case kSplitK + 4 * 16 + 1: m1d_body<4, 1, D, MT, true, true>(st.a, lds, w, target, s); break;
       case kSplitK + 3 * 16 + 1: m1d_body<3, 1, D, MT, true, true>(st.a, lds, w, target, s); break;
       case kSplitK + 2 * 16 + 1: m1d_body<2, 1, D, MT, true, true>(st.a, lds, w, target, s); break;
+      case kAct + kSplitK + 4 * 16 + 1: m1d_body<4, 1, D, MT, true, true, true>(st.a, lds, w, target, s); break;
+      case kAct + kSplitK + 3 * 16 + 1: m1d_body<3, 1, D, MT, true, true, true>(st.a, lds, w, target, s); break;
+      case kAct + kSplitK + 2 * 16 + 1: m1d_body<2, 1, D, MT, true, true, true>(st.a, lds, w, target, s); break;
       default: m1d_body<2, 8, D, MT, true>(st.a, lds, w, target, s); break;
     }
     // signal: this workgroup's outputs of steps <= s are stored (each wave waits for its own stores' acknowledgement,
@@ -748,10 +767,12 @@ __global__ void __launch_bounds__(1024, 1) i8_chain_kernel(const ChainStep* __re
 
 // up to 8 tokens (padded to 1, 2, 4 or 8 in the kernel); each segment's rows are processed in 4-row blocks (the last
 // one padded).  Returns AK_INVALID if the shape does not suit the kernel (group 64, the tokens' activations beyond the
-// LDS, a segment beyond 2 GB): the caller falls back to the any-m kernel.
-int i8_gemv_m1(int bits, const void* x, int m, const Segs& g, int k, int group, hipStream_t s) {
+// LDS, a segment beyond 2 GB): the caller falls back to the any-m kernel.  act = 1: x is the merged gate_up [m][2k] and
+// the activations are SiLU(gate) * up.
+int i8_gemv_m1(int bits, const void* x, int m, const Segs& g, int k, int group, hipStream_t s, int act) {
   if (group != kG || m < 1 || m > 8) return AK_INVALID;
   I8Args a;
+  a.act = act;
   a.segs = g;
   a.x = static_cast<const uint16_t*>(x);
   a.m = m;
@@ -786,7 +807,7 @@ int i8_gemv_m1(int bits, const void* x, int m, const Segs& g, int k, int group, 
 // more than two tokens, activations beyond the LDS, a segment beyond 2 GB): the caller then runs the steps one launch
 // each.  x[i], m[i], k[i], bits[i], segs[i], wait[i] describe step i.
 int m1d_chain_make(int nsteps, const int* bits, const void* const* x, const int* m, const int* k, const Segs* segs,
-                   const int* wait, void** table, int* mt_out, size_t* smem_out) {
+                   const int* wait, const int* act, void** table, int* mt_out, size_t* smem_out) {
   int mt = 1;
   for (int i = 0; i < nsteps; ++i) {
     if (m[i] < 1 || m[i] > 2 || bits[i] < 2 || bits[i] > 4) return AK_INVALID;
@@ -813,10 +834,11 @@ int m1d_chain_make(int nsteps, const int* bits, const void* const* x, const int*
     a.part = nullptr;
     a.cnt = nullptr;
     h[i].wait = i > 0 && wait[i] ? 1 : 0;
+    a.act = act[i];
     int nr = 0;
     size_t sks = 0, zb = 0;
     if (m1d_sk_shape(a, bits[i], mt, &nr, &sks, &zb) && nr * a.P <= num_cus()) {
-      h[i].kind = kSplitK + bits[i] * 16 + 1;
+      h[i].kind = (act[i] ? kAct : 0) + kSplitK + bits[i] * 16 + 1;
       a.wg_end[0] = nr * a.P;
       zoff[(size_t)i] = total;
       total += (zb + 255) & ~(size_t)255;
@@ -824,7 +846,7 @@ int m1d_chain_make(int nsteps, const int* bits, const void* const* x, const int*
       continue;
     }
     M1dShape sh;
-    if (plan_m1d(a, bits[i], mt, true, sh)) {
+    if (act[i] || plan_m1d(a, bits[i], mt, true, sh)) {  // SiLU(gate) * up steps: split-K shapes only
       free(h);
       return AK_INVALID;
     }

@@ -191,7 +191,10 @@ __global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
       const bool ok = u < units && t < mm && kk < k;
       xv[b] = make_uint4(0u, 0u, 0u, 0u);
       if (pass0 + b < npass) {
-        const uint4 v = *reinterpret_cast<const uint4*>(a.x + (ok ? (size_t)t * k + kk : 0));
+        // a.act: x is gate_up [mm][2k], the activation SiLU(gate) * up of the two halves
+        const size_t xo = ok ? (size_t)t * (a.act ? 2 * k : k) + kk : 0;
+        uint4 v = *reinterpret_cast<const uint4*>(a.x + xo);
+        if (a.act) v = silu_mul8_call(v, *reinterpret_cast<const uint4*>(a.x + xo + k));
         xv[b] = ok ? v : make_uint4(0u, 0u, 0u, 0u);
       }
     }
@@ -594,13 +597,15 @@ int launch_mt(I8Args a, hipStream_t s) {
 
 // 1..16 tokens (4, 8 or 16 in the kernel), 16-row blocks (the last one padded); activations beyond the LDS: split-K
 // across workgroups or chunks of stripes.  Returns AK_INVALID if the shape does not suit the kernel (group 64, a segment beyond 2 GB, a chunk of
-// one stripe beyond the LDS): the caller falls back.
-int i8_gemv_mt(int bits, const void* x, int m, const Segs& g, int k, int group, hipStream_t s) {
+// one stripe beyond the LDS): the caller falls back.  act = 1: x is the merged gate_up [m][2k] and the activations
+// are SiLU(gate) * up.
+int i8_gemv_mt(int bits, const void* x, int m, const Segs& g, int k, int group, hipStream_t s, int act) {
   if (group != kG || m < 1 || m > 16) return AK_INVALID;
 #ifdef AK_NO_MT
   return AK_INVALID;
 #endif
   I8Args a;
+  a.act = act;
   a.segs = g;
   a.x = static_cast<const uint16_t*>(x);
   a.m = m;

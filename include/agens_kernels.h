@@ -153,6 +153,16 @@ int ak_silu_mul(const void* gate_up, void* out, int tokens, int inter,
 int ak_silu_mul_part(const void* gate_up_part, void* out, int inter, int lo, int np,
                      void* stream);               /* agens_kernels.h:113, silu_mul.cu:58-64 */
 
+/* ---------------------------------------------------------------------------------------------- fused SiLU(gate) * up
+ * No counterpart in the reference: ak_silu_mul followed by ak_wq_gemv_kt_multi in one launch, for the down projection
+ * of a decoder layer (the reference runs the two, kernels/m1/m1_model.cu:2583).  y[t] (row stride ldy; 0: n) =
+ * W . act[t], act[t][i] = bf16(SiLU(gate_up[t][i]) * gate_up[t][inter + i]) (ak_silu_mul's value, bit for bit),
+ * gate_up bf16 [m][2 inter]; W the KT layout of an n x inter linear.  Results are bit-identical to ak_silu_mul
+ * followed by ak_wq_gemv_kt_multi.  The default numerics at group 128 only: otherwise (group 64, the exact path)
+ * it returns 1 and the caller runs the two calls. */
+int ak_wq_gemv_kt_silu(int bits, const void* gate_up, int m, const void* wt, const void* st, void* y, int n, int ldy,
+                       int inter, int group, void* stream);
+
 /* ---------------------------------------------------------------------------------------------- chained GEMV steps
  * No single counterpart in the reference: it replaces a run of ak_wq_gemv_kt_multi launches joined by programmatic
  * dependent launch edges in a captured graph (reference: ak_graph_pdl, kernels/src/runtime.cu:198-230, and the
@@ -181,6 +191,7 @@ typedef struct ak_wq_step {
   int n[4];
   int ldy[4];
   int independent;
+  int act; /* 1: x is the merged gate_up [m][2k] and the step's activations are SiLU(gate) * up (ak_wq_gemv_kt_silu) */
 } ak_wq_step;
 int ak_wq_chain_create(const ak_wq_step* steps, int nsteps, void** chain);
 int ak_wq_chain_run(void* chain, void* stream);

@@ -197,7 +197,7 @@ class WqStep(ctypes.Structure):
     """ak_wq_step of include/agens_kernels.h (one GEMV step of a chain)."""
     _fields_ = [("bits", c_int), ("m", c_int), ("nseg", c_int), ("k", c_int), ("group", c_int), ("bf16w", c_int),
                 ("x", c_void_p), ("wt", c_void_p * 4), ("st", c_void_p * 4), ("y", c_void_p * 4), ("n", c_int * 4),
-                ("ldy", c_int * 4), ("independent", c_int)]
+                ("ldy", c_int * 4), ("independent", c_int), ("act", c_int)]
 
 
 def _addr(v):
@@ -206,7 +206,7 @@ def _addr(v):
     return v.value if isinstance(v, c_void_p) else v
 
 
-def wq_step(bits, x, m, lins, ys, k, group=128, ldy=None, independent=0, bf16w=0):
+def wq_step(bits, x, m, lins, ys, k, group=128, ldy=None, independent=0, bf16w=0, act=0):
     """A chain step over the Linear segments `lins` with outputs `ys` (Dev or addresses), x a Dev or an address."""
     st = WqStep()
     st.bits, st.m, st.nseg, st.k, st.group, st.bf16w = bits, m, len(lins), k, group, bf16w
@@ -215,6 +215,7 @@ def wq_step(bits, x, m, lins, ys, k, group=128, ldy=None, independent=0, bf16w=0
         st.wt[i], st.st[i], st.y[i], st.n[i] = L.wt.p.value, L.st.p.value, _addr(y), L.n
         st.ldy[i] = ldy[i] if ldy else 0
     st.independent = independent
+    st.act = act
     return st
 
 
@@ -299,6 +300,7 @@ def kernels():
             "ak_i8_gemv": (i, [vp, vp, vp, vp, i, i, i, i, vp]),
             "ak_bf16_gemv_bi": (i, [vp, vp, vp, vp, i, i, i, vp]),
             "ak_silu_mul": (i, [vp, vp, i, i, vp]),
+            "ak_wq_gemv_kt_silu": (i, [i, vp, i, vp, vp, vp, i, i, i, i, vp]),
             "ak_silu_mul_part": (i, [vp, vp, i, i, i, vp]),
             "ak_bf16_gemv_bi_ld": (i, [vp, vp, vp, vp, i, i, i, ctypes.c_long, vp]),
             "ak_wq_chain_create": (i, [ctypes.POINTER(WqStep), i, ctypes.POINTER(c_void_p)]),
