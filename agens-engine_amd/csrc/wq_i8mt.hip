@@ -102,7 +102,8 @@ __host__ __device__ inline int mt_meta_bytes(int ngroups, int nt) { return nt * 
 // SK (split-K across workgroups, for activations beyond the LDS, one segment): workgroup (r, p) computes stripe p of the
 // rows of range r, converting only that stripe's activations; it writes its stripe partials with device-coherent
 // stores, and the last of the range's P workgroups (device-scope counter) adds them in stripe order and writes y.
-template <int BITS, int SPLIT, int DEPTH, int NT, bool CH, bool SK = false>
+// ACT (split-K launches only): x is the merged gate_up [m][2k], the activations SiLU(gate) * up (ak_silu_mul's value)
+template <int BITS, int SPLIT, int DEPTH, int NT, bool CH, bool SK = false, bool ACT = false>
 __global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
   static_assert((!CH && !SK) || SPLIT == 1, "chunked and split launches give every wave whole stripes of its blocks");
   static_assert(!(CH && SK), "one of the two");
@@ -191,10 +192,9 @@ __global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
       const bool ok = u < units && t < mm && kk < k;
       xv[b] = make_uint4(0u, 0u, 0u, 0u);
       if (pass0 + b < npass) {
-        // a.act: x is gate_up [mm][2k], the activation SiLU(gate) * up of the two halves
-        const size_t xo = ok ? (size_t)t * (a.act ? 2 * k : k) + kk : 0;
+        const size_t xo = ok ? (size_t)t * (ACT ? 2 * k : k) + kk : 0;
         uint4 v = *reinterpret_cast<const uint4*>(a.x + xo);
-        if (a.act) v = silu_mul8_call(v, *reinterpret_cast<const uint4*>(a.x + xo + k));
+        if constexpr (ACT) v = silu_mul8(v, *reinterpret_cast<const uint4*>(a.x + xo + k));
         xv[b] = ok ? v : make_uint4(0u, 0u, 0u, 0u);
       }
     }
@@ -476,10 +476,10 @@ size_t mt_block_bytes(int P, int split, int nt) {  // per 16-row block: outputs,
   return (size_t)4 * nt * 16 * 2 + (split > 1 ? (size_t)P * 4 * nt * 16 * 4 + 4 : 0);
 }
 
-template <int BITS, int SPLIT, int NT, bool CH, bool SK = false>
+template <int BITS, int SPLIT, int NT, bool CH, bool SK = false, bool ACT = false>
 void launch_mt_split(const I8Args& a, int grid, size_t smem, hipStream_t s) {
   constexpr int DEPTH = NT > 2 ? 1 : 2;  // items in flight per wave (16 tokens: their accumulators take the registers)
-  hipLaunchKernelGGL((i8_mt_kernel<BITS, SPLIT, DEPTH, NT, CH, SK>), dim3(grid), dim3(1024), smem, s, a);
+  hipLaunchKernelGGL((i8_mt_kernel<BITS, SPLIT, DEPTH, NT, CH, SK, ACT>), dim3(grid), dim3(1024), smem, s, a);
 }
 
 // groups of the largest of nch chunks of stripes
@@ -548,10 +548,14 @@ int launch_mt(I8Args a, hipStream_t s) {
       }
       b.cnt = static_cast<int*>(z);
       b.part = reinterpret_cast<float*>(static_cast<uint8_t*>(z) + 4096);
-      launch_mt_split<BITS, 1, NT, false, true>(b, b.wg_end[g.nseg - 1], smem, s);
+      if (a.act)
+        launch_mt_split<BITS, 1, NT, false, true, true>(b, b.wg_end[g.nseg - 1], smem, s);
+      else
+        launch_mt_split<BITS, 1, NT, false, true>(b, b.wg_end[g.nseg - 1], smem, s);
       return (int)hipGetLastError();
     }
   }
+  if (a.act) return AK_INVALID;  // the SiLU(gate) * up activation: split-K launches only (the caller falls back)
   if (x_bytes <= 140 * 1024) {
     // the whole activation image fits: tasks per block = fewest quad rounds for the busiest wave, a task's overhead
     // counted as about one quad

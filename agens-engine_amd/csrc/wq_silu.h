@@ -23,8 +23,5 @@ __device__ __forceinline__ uint32_t silu_mul_pair(uint32_t g, uint32_t u) {
 __device__ __forceinline__ uint4 silu_mul8(const uint4 g, const uint4 u) {
   return make_uint4(silu_mul_pair(g.x, u.x), silu_mul_pair(g.y, u.y), silu_mul_pair(g.z, u.z), silu_mul_pair(g.w, u.w));
 }
-// the same as a call: the GEMV kernels' activation loads use this one, so that the exp code is not inlined into every
-// instance of their load loops (the chained kernel holds one instance per step kind)
-static __device__ __noinline__ uint4 silu_mul8_call(const uint4 g, const uint4 u) { return silu_mul8(g, u); }
 
 }  // namespace agq
