@@ -19,6 +19,23 @@ struct I8Args {
   int act = 0;    // 1: x is the merged gate_up [m][2k] and the activations are SiLU(gate) * up (wq_silu.h)
 };
 
+// The P (<= 8) stripe partials of one output of a split-K launch, at float offsets off + q * stride (q < P) of base,
+// written by other workgroups with device-coherent stores: loaded device-coherently (sc1: not served from a stale L2
+// line) all at once, then added in stripe order from stripe 0.  One dependent round trip instead of P.
+__device__ __forceinline__ float sum_stripe_partials(const float* base, size_t off, size_t stride, int P) {
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, 0x7FFFFFFF, 0x00020000);
+  float v[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q)
+    v[q] = q < P ? __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (int)((off + q * stride) * 4), 0, 16)) : 0.f;
+  float y = v[0];
+#pragma unroll
+  for (int q = 1; q < 8; ++q)
+    if (q < P) y += v[q];
+  return y;
+}
+
 // Stripes are contiguous runs of whole 1024-input tiles: with nt = nquad / qpt tiles, P = min(8, nt) stripes and stripe
 // p = tiles [p * nt / P, (p + 1) * nt / P), i.e. quads [qpt * (p * nt / P), qpt * ((p + 1) * nt / P)).
 __host__ __device__ inline int stripe_count(int nquad, int qpt) { return nquad / qpt < 8 ? nquad / qpt : 8; }

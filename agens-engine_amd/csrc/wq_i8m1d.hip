@@ -216,7 +216,13 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
   const int rr = c >> 2, vv = c & 3;  // B role: row of the block, group of the quad
   const Segs& sgs = a.segs;
 
-  if (CHAIN && (int)blockIdx.x >= AK_PICK(sgs.nseg - 1, a.wg_end)) return;  // no rows of this step
+  // no rows of this step: the workgroup still passes the step's wait (wave 0 polls; the chain's barrier after the step
+  // holds the other waves), so that a later step declared independent never reads what the steps before this one
+  // write before they have written it
+  if (CHAIN && (int)blockIdx.x >= AK_PICK(sgs.nseg - 1, a.wg_end)) {
+    if (wait && (threadIdx.x >> 6) == 0) chain_poll(target);
+    return;
+  }
   // this workgroup's segment and its blocks [b_lo, b_lo + nb) of that segment (SK: row range r, stripe psk; the
   // ranges are wg_end[0] / P)
   int sg = 0;
@@ -554,11 +560,8 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
     if (!*last) return;
     for (int i = tid; i < MT * nb * 4; i += 64 * nwv) {
       const int t = MT == 1 ? 0 : i / (nb * 4), o = i - t * nb * 4;
-      const float* src = a.part + ((size_t)t * n_b4 + b_lo) * 4 + o;
-      float y = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      for (int q = 1; q < P; ++q)
-        y += __hip_atomic_load(src + (size_t)q * MT * n_b4 * 4, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      yl[i] = f2bf(y);
+      const size_t off = ((size_t)t * n_b4 + b_lo) * 4 + o;
+      yl[i] = f2bf(sum_stripe_partials(a.part, off, (size_t)MT * n_b4 * 4, P));
     }
     __syncthreads();
   }

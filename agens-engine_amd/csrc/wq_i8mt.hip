@@ -445,15 +445,13 @@ __global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
       if (old == P - 1) __hip_atomic_store(scnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next launch
     }
     __syncthreads();
+    AK_M1_STAMP(4);
     if (!*last) return;
     __syncthreads();  // every thread has read the flag before the outputs overwrite it
     for (int i = tid; i < nb * MP * 16; i += 64 * nwv) {
       const int bl = i / (MP * 16), o = i - bl * MP * 16, t = o >> 4;
-      const float* src = spart + ((size_t)t * n_b16 + b_lo + bl) * 16 + (o & 15);
-      float y = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      for (int q = 1; q < P; ++q)
-        y += __hip_atomic_load(src + (size_t)q * MP * n_b16 * 16, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      yl[i] = f2bf(y);
+      const size_t off = ((size_t)t * n_b16 + b_lo + bl) * 16 + (o & 15);
+      yl[i] = f2bf(sum_stripe_partials(spart, off, (size_t)MP * n_b16 * 16, P));
     }
   }
   if constexpr (CH) {
