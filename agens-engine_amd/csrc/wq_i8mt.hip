@@ -291,10 +291,12 @@ __global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
     }
   };
   convert(0);
+  AK_M1_STAMP(5);
   for (int p0 = XB; p0 < npass; p0 += XB) {
     xload(p0);
     convert(p0);
   }
+  AK_M1_STAMP(6);
   __syncthreads();
   AK_M1_STAMP(2);
 

@@ -219,3 +219,31 @@ def test_chain_at_decode_shapes_matches_launches(m):
     last = got[-1][0].astype(np.uint32) << 16
     f = last.view(np.float32)
     assert np.all(np.isfinite(f)) and np.std(f) > 0.05
+
+
+def test_chain_independent_step_after_a_step_most_workgroups_skip():
+    """A: x -> y1 (large), B (dependent): y1[:5120] -> y2 with 16 rows (most workgroups have no rows in it), C (independent of
+    B): y1 -> y3 on every workgroup.  C reads A's output, so every workgroup must have passed B's wait, also those
+    with no rows in B; the same steps one launch each give the reference values.  Two runs in a row."""
+    K = kernels()
+    k = 5120
+    # B: k = 5120 (the first 5120 outputs of A), 16 rows = 4 blocks: 4 workgroups have rows, 252 skip it
+    a, b, c = Lin(21, 27648, k, 3), Lin(23, 16, k, 4), Lin(25, 4096, 27648, 2)
+    x = Dev(k * 2)
+    y1, y2, y3 = Dev(27648 * 2), Dev(16 * 2), Dev(4096 * 2)
+    steps = [wq_step(3, x, 1, [a.L], [y1], k), wq_step(4, y1, 1, [b.L], [y2], k),
+             wq_step(2, y1, 1, [c.L], [y3], 27648, independent=1)]
+    ch = Chain(steps)
+    assert ch.chained
+    for rep in range(2):
+        xh = gen_x(123 + rep, k)
+        check(K.ak_memcpy_h2d(x.p, xh.ctypes.data, xh.nbytes), "h2d")
+        ch.run()
+        check(K.ak_synchronize(), "sync")
+        assert K.ak_wq_chain_status() == 0
+        got = [y.get(np.uint16, n) for y, n in ((y1, 27648), (y2, 16), (y3, 4096))]
+        for lin, xin, kk, y in ((a, x, k, y1), (b, y1, k, y2), (c, y1, 27648, y3)):
+            gemv(lin.bits, xin.p, 1, [lin.L], kk, 128, ys=[y])
+        check(K.ak_synchronize(), "sync")
+        for g, (y, n, name) in zip(got, ((y1, 27648, "A"), (y2, 16, "B"), (y3, 4096, "C"))):
+            assert np.array_equal(g, y.get(np.uint16, n)), f"run {rep} step {name}"
