@@ -45,29 +45,39 @@ __device__ __forceinline__ uint4 load_chunk(const void* __restrict__ wt, size_t 
                     (spread2(lo.y >> 16) | (spread1(h >> 24) << 2)) + 0x44444444u);
 }
 
-// nibble i of w as an exact fp32 (q = nibble - 8): 2^23 + nibble via the exponent field, minus 2^23 + 8
-__device__ __forceinline__ float nibf(uint32_t w, int i) {
-  return __uint_as_float(0x4B000000u | ((w >> (4 * i)) & 0xFu)) - 8388616.0f;
+// nibble i of w as an exact fp32 q = nibble - 8, from w8 = w ^ 0x88888888 (nibble ^ 8 is q as a 4-bit two's
+// complement field): a sign-extending field extract (a shift pair) and one conversion.  Not __builtin_amdgcn_sbfe:
+// this toolchain converts its result as if it were unsigned (v_cvt_f32_u32), which is wrong for the negative codes.
+__device__ __forceinline__ float nibq(uint32_t w8, int i) { return (float)((int)(w8 << (28 - 4 * i)) >> 28); }
+
+// the 32 inputs of a lane chunk as fp32 (XF: already fp32 in LDS; else 16 words of bf16 pairs)
+struct ChunkX {
+  float v[32];
+};
+__device__ __forceinline__ void chunk_x_bf16(const uint32_t* xp, ChunkX& cx) {
+#pragma unroll
+  for (int p = 0; p < 16; ++p) cx.v[2 * p] = __uint_as_float(xp[p] << 16), cx.v[2 * p + 1] = __uint_as_float(xp[p] & 0xFFFF0000u);
 }
 
-// dot of one nibble word (8 inputs) with 4 bf16 pairs: the fixed fma chain
+// dot of one nibble word (8 inputs) with its 8 inputs: the fixed fma chain
 template <bool BW>
-__device__ __forceinline__ float dot8(uint32_t w, const uint32_t* xp, float sc) {
+__device__ __forceinline__ float dot8(uint32_t w, const float* xv, float sc) {
+  const uint32_t w8 = w ^ 0x88888888u;
   float s = 0.f;
 #pragma unroll
   for (int p = 0; p < 4; ++p) {
-    float a = nibf(w, 2 * p), b = nibf(w, 2 * p + 1);
+    float a = nibq(w8, 2 * p), b = nibq(w8, 2 * p + 1);
     if (BW) a = bf2f(f2bf(a * sc)), b = bf2f(f2bf(b * sc));
-    s = fmaf(__uint_as_float(xp[p] << 16), a, s);
-    s = fmaf(__uint_as_float(xp[p] & 0xFFFF0000u), b, s);
+    s = fmaf(xv[2 * p], a, s);
+    s = fmaf(xv[2 * p + 1], b, s);
   }
   return s;
 }
 
 template <bool BW>
-__device__ __forceinline__ float chunk_step(const uint4& w, const uint32_t* xp, float sc, float acc) {
-  const float d = dot8<BW>(w.x, xp, sc) + dot8<BW>(w.y, xp + 4, sc) + dot8<BW>(w.z, xp + 8, sc) +
-                  dot8<BW>(w.w, xp + 12, sc);
+__device__ __forceinline__ float chunk_step(const uint4& w, const ChunkX& cx, float sc, float acc) {
+  const float d = dot8<BW>(w.x, cx.v, sc) + dot8<BW>(w.y, cx.v + 8, sc) + dot8<BW>(w.z, cx.v + 16, sc) +
+                  dot8<BW>(w.w, cx.v + 24, sc);
   return BW ? acc + d : fmaf(d, sc, acc);
 }
 
@@ -77,14 +87,24 @@ __device__ __forceinline__ float half_wave_sum(float v) {
   return v;
 }
 
-// KT layout, m tokens (MT = 1: x staged in LDS chunk-transposed; MT > 1: up to MT tokens, x read from global).
-template <int BITS, int G, bool BW, int MT>
+// KT layout, m tokens (MT = 1: x staged in LDS chunk-transposed, XF: as fp32, 4 inputs per 16-byte read; MT > 1: up
+// to MT tokens, x read from global).
+template <int BITS, int G, bool BW, int MT, bool XF = false>
 __global__ void __launch_bounds__(kThreads) exact_kernel(const uint16_t* __restrict__ x, int m, const Segs segs,
                                                          int k) {
   extern __shared__ uint32_t xs[];
   constexpr int SPT = 1024 / G, CPG = G / 32;
   const int kp = kpad(k), chunks = kp >> 5, tiles = kp >> 10, kc = k >> 5;
-  if (MT == 1) {
+  if (MT == 1 && XF) {  // [quad q of 4 inputs][chunk c] float4: chunk c's inputs 4q .. 4q + 3
+    const uint32_t* xw = reinterpret_cast<const uint32_t*>(x);
+    float4* const x4 = reinterpret_cast<float4*>(xs);
+    for (int i = threadIdx.x; i < (kp >> 2); i += kThreads) {
+      const uint32_t a = 2 * i < (k >> 1) ? xw[2 * i] : 0u, b = 2 * i + 1 < (k >> 1) ? xw[2 * i + 1] : 0u;
+      x4[(i & 7) * chunks + (i >> 3)] = make_float4(__uint_as_float(a << 16), __uint_as_float(a & 0xFFFF0000u),
+                                                    __uint_as_float(b << 16), __uint_as_float(b & 0xFFFF0000u));
+    }
+    __syncthreads();
+  } else if (MT == 1) {
     const uint32_t* xw = reinterpret_cast<const uint32_t*>(x);
     for (int i = threadIdx.x; i < (kp >> 1); i += kThreads) xs[(i & 15) * chunks + (i >> 4)] = i < (k >> 1) ? xw[i] : 0u;
     __syncthreads();
@@ -105,11 +125,22 @@ __global__ void __launch_bounds__(kThreads) exact_kernel(const uint16_t* __restr
       const uint4 w = load_chunk<BITS>(wt, rec, lane);
       const float sc = bf2f(st[rec * SPT + lane / CPG]);
       const int c = t * 32 + lane;
-      if (MT == 1) {
+      if (MT == 1 && XF) {
+        ChunkX cx;
+        const float4* x4 = reinterpret_cast<const float4*>(xs);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const float4 f = x4[q * chunks + c];
+          cx.v[4 * q] = f.x, cx.v[4 * q + 1] = f.y, cx.v[4 * q + 2] = f.z, cx.v[4 * q + 3] = f.w;
+        }
+        acc[0] = chunk_step<BW>(w, cx, sc, acc[0]);
+      } else if (MT == 1) {
         uint32_t xp[16];
 #pragma unroll
         for (int p = 0; p < 16; ++p) xp[p] = xs[p * chunks + c];
-        acc[0] = chunk_step<BW>(w, xp, sc, acc[0]);
+        ChunkX cx;
+        chunk_x_bf16(xp, cx);
+        acc[0] = chunk_step<BW>(w, cx, sc, acc[0]);
       } else {
 #pragma unroll
         for (int j = 0; j < MT; ++j) {
@@ -126,7 +157,9 @@ __global__ void __launch_bounds__(kThreads) exact_kernel(const uint16_t* __restr
 #pragma unroll
             for (int p = 0; p < 16; ++p) xp[p] = 0u;
           }
-          acc[j] = chunk_step<BW>(w, xp, sc, acc[j]);
+          ChunkX cx;
+          chunk_x_bf16(xp, cx);
+          acc[j] = chunk_step<BW>(w, cx, sc, acc[j]);
         }
       }
     }
@@ -159,7 +192,9 @@ __global__ void __launch_bounds__(kThreads) exact_ct_kernel(const uint16_t* __re
       uint32_t xp[16];
 #pragma unroll
       for (int p = 0; p < 16; ++p) xp[p] = xs[p * chunks + c];
-      acc = chunk_step<false>(w, xp, sc, acc);
+      ChunkX cx;
+      chunk_x_bf16(xp, cx);
+      acc = chunk_step<false>(w, cx, sc, acc);
     }
     const float v = half_wave_sum(acc);
     if (lane == 0) y[o] = f2bf(v);
@@ -168,11 +203,17 @@ __global__ void __launch_bounds__(kThreads) exact_ct_kernel(const uint16_t* __re
 
 template <int BITS, int G, bool BW, int MT>
 int launch_exact(const void* x, int m, const Segs& g, int k, hipStream_t s) {
-  const size_t smem = MT == 1 ? (size_t)kpad(k) * 2 : 0;
+  // one token: x as fp32 in LDS while that leaves room for several workgroups per CU (k <= 8192), else as bf16
+  const bool xf = MT == 1 && kpad(k) <= 8192;
+  const size_t smem = MT == 1 ? (size_t)kpad(k) * (xf ? 4 : 2) : 0;
   const int rows = g.end[g.nseg - 1];
   const int want = (rows + kThreads / 32 - 1) / (kThreads / 32), cap = num_cus() * 8;
-  hipLaunchKernelGGL((exact_kernel<BITS, G, BW, MT>), dim3(want < cap ? want : cap), dim3(kThreads), smem, s,
-                     static_cast<const uint16_t*>(x), m, g, k);
+  if (xf)
+    hipLaunchKernelGGL((exact_kernel<BITS, G, BW, MT, true>), dim3(want < cap ? want : cap), dim3(kThreads), smem, s,
+                       static_cast<const uint16_t*>(x), m, g, k);
+  else
+    hipLaunchKernelGGL((exact_kernel<BITS, G, BW, MT>), dim3(want < cap ? want : cap), dim3(kThreads), smem, s,
+                       static_cast<const uint16_t*>(x), m, g, k);
   return (int)hipGetLastError();
 }
 
