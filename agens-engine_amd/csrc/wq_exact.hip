@@ -30,19 +30,36 @@ __device__ __forceinline__ uint32_t spread1(uint32_t v) {
   return (v ^ (v << 3)) & 0x11111111u;
 }
 
+// a lane chunk's raw KT words (W4: the nibble chunk; W3: two-bit plane words + third-bit plane word; W2: plane words),
+// and their decoding into W4 nibble words (nibble = q + 8) -- separate, so that a chunk can be requested a tile ahead
+// and decoded when it is used
+struct RawChunk {
+  uint4 w;  // W4: the chunk; W2 / W3: .x .y the two-bit plane, .z the third-bit plane (W3)
+};
 template <int BITS>
-__device__ __forceinline__ uint4 load_chunk(const void* __restrict__ wt, size_t rec, int c) {
-  if (BITS == 4) return ld_stream(reinterpret_cast<const uint4*>(wt) + rec * 32 + c);
-  const uint32_t* r = reinterpret_cast<const uint32_t*>(wt) + rec * (32 * BITS);
-  const uint2 lo = reinterpret_cast<const uint2*>(r)[c];
+__device__ __forceinline__ RawChunk load_raw_chunk(const void* __restrict__ wt, size_t rec, int c) {
+  RawChunk r;
+  if (BITS == 4) {
+    r.w = ld_stream(reinterpret_cast<const uint4*>(wt) + rec * 32 + c);
+  } else {
+    const uint32_t* p = reinterpret_cast<const uint32_t*>(wt) + rec * (32 * BITS);
+    const uint2 lo = reinterpret_cast<const uint2*>(p)[c];
+    r.w = make_uint4(lo.x, lo.y, BITS == 3 ? p[64 + c] : 0u, 0u);
+  }
+  return r;
+}
+template <int BITS>
+__device__ __forceinline__ uint4 decode_chunk(const RawChunk& r) {
+  if (BITS == 4) return r.w;
+  const uint32_t lx = r.w.x, ly = r.w.y;
   if (BITS == 2)
-    return make_uint4(spread2(lo.x) + 0x66666666u, spread2(lo.x >> 16) + 0x66666666u, spread2(lo.y) + 0x66666666u,
-                      spread2(lo.y >> 16) + 0x66666666u);
-  const uint32_t h = r[64 + c];
-  return make_uint4((spread2(lo.x) | (spread1(h) << 2)) + 0x44444444u,
-                    (spread2(lo.x >> 16) | (spread1(h >> 8) << 2)) + 0x44444444u,
-                    (spread2(lo.y) | (spread1(h >> 16) << 2)) + 0x44444444u,
-                    (spread2(lo.y >> 16) | (spread1(h >> 24) << 2)) + 0x44444444u);
+    return make_uint4(spread2(lx) + 0x66666666u, spread2(lx >> 16) + 0x66666666u, spread2(ly) + 0x66666666u,
+                      spread2(ly >> 16) + 0x66666666u);
+  const uint32_t h = r.w.z;
+  return make_uint4((spread2(lx) | (spread1(h) << 2)) + 0x44444444u,
+                    (spread2(lx >> 16) | (spread1(h >> 8) << 2)) + 0x44444444u,
+                    (spread2(ly) | (spread1(h >> 16) << 2)) + 0x44444444u,
+                    (spread2(ly >> 16) | (spread1(h >> 24) << 2)) + 0x44444444u);
 }
 
 // nibble i of w as an exact fp32 q = nibble - 8, from w8 = w ^ 0x88888888 (nibble ^ 8 is q as a 4-bit two's
@@ -120,10 +137,19 @@ __global__ void __launch_bounds__(kThreads) exact_kernel(const uint16_t* __restr
     float acc[MT];
 #pragma unroll
     for (int j = 0; j < MT; ++j) acc[j] = 0.f;
+    // the next tile's chunk and scale are requested before this tile is computed
+    RawChunk wn = load_raw_chunk<BITS>(wt, o, lane);
+    uint16_t sn = st[(size_t)o * SPT + lane / CPG];
     for (int t = 0; t < tiles; ++t) {
-      const size_t rec = (size_t)t * n + o;
-      const uint4 w = load_chunk<BITS>(wt, rec, lane);
-      const float sc = bf2f(st[rec * SPT + lane / CPG]);
+      const RawChunk wr = wn;
+      const uint16_t sr = sn;
+      if (t + 1 < tiles) {
+        const size_t rn = (size_t)(t + 1) * n + o;
+        wn = load_raw_chunk<BITS>(wt, rn, lane);
+        sn = st[rn * SPT + lane / CPG];
+      }
+      const uint4 w = decode_chunk<BITS>(wr);
+      const float sc = bf2f(sr);
       const int c = t * 32 + lane;
       if (MT == 1 && XF) {
         ChunkX cx;
