@@ -130,6 +130,49 @@ int agb_gen_f32(uint64_t seed, size_t count, float sa, float sb, void* s, void* 
   return (int)hipGetLastError();
 }
 
+// ak_bf16_gemv_bi over `ncopies` weight copies in turn (w + c * n * k), timed as agb_time_i8_gemv
+int agb_time_bi_gemv(const void* x, const void* w, void* y, int m, int n, int k, int ncopies, int warmup, int steps,
+                     float* ms) {
+  hipStream_t s;
+  int e = (int)hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+  if (e) return e;
+  auto one = [&](int i) {
+    return ak_bf16_gemv_bi(x, (const uint16_t*)w + (size_t)(i % ncopies) * n * k, nullptr, y, m, n, k, s);
+  };
+  for (int i = 0; i < warmup && !e; ++i) e = one(i);
+  hipGraph_t g = nullptr;
+  hipGraphExec_t ge = nullptr;
+  bool cap = false;
+  if (!e) {
+    e = (int)hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+    cap = !e;
+  }
+  for (int i = 0; i < steps && !e; ++i) e = one(i);
+  if (cap) {
+    const int e2 = (int)hipStreamEndCapture(s, &g);
+    if (!e) e = e2;
+  }
+  if (!e) e = (int)hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+  if (!e) e = (int)hipGraphLaunch(ge, s);
+  hipEvent_t a, b;
+  hipEventCreate(&a);
+  hipEventCreate(&b);
+  if (!e) e = (int)hipEventRecord(a, s);
+  if (!e) e = (int)hipGraphLaunch(ge, s);
+  if (!e) e = (int)hipEventRecord(b, s);
+  if (!e) e = (int)hipEventSynchronize(b);
+  float t = 0.f;
+  if (!e) e = (int)hipEventElapsedTime(&t, a, b);
+  *ms = t / steps;
+  hipEventDestroy(a);
+  hipEventDestroy(b);
+  if (ge) hipGraphExecDestroy(ge);
+  if (g) hipGraphDestroy(g);
+  hipStreamSynchronize(s);
+  hipStreamDestroy(s);
+  return e;
+}
+
 // ak_i8_gemv over `ncopies` weight copies in turn (w + c * n * k, scale + c * n), `steps` launches captured in one
 // hipGraph after `warmup` eager ones; *ms = the mean time per launch (HIP events on the launching stream).
 int agb_time_i8_gemv(const void* x, const void* w, const void* scale, void* y, int m, int n, int k, int ncopies,

@@ -6,7 +6,8 @@
 // same for every m).  The reference's bits come from its MMA instruction's internal accumulation, which no other
 // hardware reproduces; this kernel keeps the reference's contract instead -- fp32 accumulation, the bias added in fp32
 // before the one bf16 rounding, and an order that does not depend on m:
-//   - a workgroup owns 16 rows; its 8 waves take the 64-input k-steps s = w, w + 8, w + 16, ... (wave w), each step two
+//   - a workgroup owns 16 rows; its 8 waves take the 64-input k-steps s = w, w + 8, w + 16, ... (wave w; four steps'
+//     loads issued at a time), each step two
 //     v_mfma_f32_16x16x32_bf16 (inputs [64 s, 64 s + 32) then [64 s + 32, 64 s + 64)) accumulating in fp32;
 //   - the MFMA's A operand is 16 weight rows, its B operand 16 tokens: the columns of the result are independent, so a
 //     token's sums do not depend on the other tokens; more than 16 tokens are more B tiles of the same steps;
@@ -46,22 +47,49 @@ __global__ void __launch_bounds__(kWaves * 64) bi_gemv_kernel(const uint16_t* __
 #pragma unroll
   for (int t = 0; t < TT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   const int steps = (k + 63) >> 6;
-  for (int s = wave; s < steps; s += kWaves) {
-    const int k0 = 64 * s;
-    const bool two = k0 + 32 < k;  // k % 32 == 0: the step's second slice exists unless k ends at k0 + 32
-    const uint4 z = make_uint4(0u, 0u, 0u, 0u);
-    const uint4 a0 = rok ? *reinterpret_cast<const uint4*>(wr + k0) : z;
-    const uint4 a1 = rok && two ? *reinterpret_cast<const uint4*>(wr + k0 + 32) : z;
+  const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+  // KU of the wave's steps at a time: their weight loads (and with one token tile their activation loads) are issued
+  // together, then their MFMAs in step order -- the same chain as one step at a time
+  constexpr int KU = 4;
+  for (int s0 = wave; s0 < steps; s0 += kWaves * KU) {
+    uint4 a0[KU], a1[KU], b0[KU], b1[KU];
 #pragma unroll
-    for (int t = 0; t < TT; ++t) {
-      const int tok = 16 * t + (lane & 15);
-      const bool tk = tok < m;
-      const uint16_t* xr = x + (size_t)(tk ? tok : 0) * k + kq + k0;
-      const uint4 b0 = tk ? *reinterpret_cast<const uint4*>(xr) : z;
-      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a0), as_bf16x8(b0), acc[t], 0, 0, 0);
-      if (two) {
-        const uint4 b1 = tk ? *reinterpret_cast<const uint4*>(xr + 32) : z;
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a1), as_bf16x8(b1), acc[t], 0, 0, 0);
+    for (int u = 0; u < KU; ++u) {
+      // unconditional 16-byte loads at clamped (always valid) offsets, zeros selected afterwards: a conditional load
+      // would be split into guarded dword loads
+      const int s = s0 + u * kWaves, k0 = 64 * s;
+      const bool in = s < steps, two = k0 + 32 < k;
+      const int ka = in ? k0 : 0, kb = in && two ? k0 + 32 : 0;
+      const u32x4 va = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wr + ka));
+      const u32x4 vb = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wr + kb));
+      a0[u] = rok && in ? make_uint4(va[0], va[1], va[2], va[3]) : z;
+      a1[u] = rok && in && two ? make_uint4(vb[0], vb[1], vb[2], vb[3]) : z;
+      if constexpr (TT == 1) {
+        const int tok = lane & 15;
+        const uint16_t* xr = x + (size_t)(tok < m ? tok : 0) * k + kq;
+        const uint4 xa = *reinterpret_cast<const uint4*>(xr + ka), xb = *reinterpret_cast<const uint4*>(xr + kb);
+        b0[u] = tok < m && in ? xa : z;
+        b1[u] = tok < m && in && two ? xb : z;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < KU; ++u) {
+      const int s = s0 + u * kWaves, k0 = 64 * s;
+      if (s >= steps) break;
+      const bool two = k0 + 32 < k;  // k % 32 == 0: the step's second slice exists unless k ends at k0 + 32
+#pragma unroll
+      for (int t = 0; t < TT; ++t) {
+        uint4 xb0 = b0[u], xb1 = b1[u];
+        if constexpr (TT > 1) {
+          const int tok = 16 * t + (lane & 15);
+          const bool tk = tok < m;
+          const uint16_t* xr = x + (size_t)(tk ? tok : 0) * k + kq + k0;
+          const uint4 xa = *reinterpret_cast<const uint4*>(xr), xb = *reinterpret_cast<const uint4*>(xr + (two ? 32 : 0));
+          xb0 = tk ? xa : z;
+          xb1 = tk && two ? xb : z;
+        }
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a0[u]), as_bf16x8(xb0), acc[t], 0, 0, 0);
+        if (two) acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a1[u]), as_bf16x8(xb1), acc[t], 0, 0, 0);
       }
     }
   }

@@ -10,7 +10,7 @@ reference's int4 container and repacked by ak_wq_repack_kt; inputs are resident 
 
 Effective bytes per launch = packed weights + bf16 scales + bf16 x + bf16 y (the algorithmic bytes).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--m 1] [--config sweep|0|1|2|3|i8] [--no-cpu] [--eager]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--m 1] [--config sweep|0|1|2|3|i8|bi] [--no-cpu] [--eager]
 """
 import argparse
 import ctypes
@@ -63,6 +63,7 @@ def load_libs():
         ("agb_gen_i8", i, [ctypes.c_uint64, sz, vp, vp]),
         ("agb_gen_f32", i, [ctypes.c_uint64, sz, ctypes.c_float, ctypes.c_float, vp, vp]),
         ("agb_time_i8_gemv", i, [vp, vp, vp, vp, i, i, i, i, i, i, ctypes.POINTER(ctypes.c_float)]),
+        ("agb_time_bi_gemv", i, [vp, vp, vp, i, i, i, i, i, i, ctypes.POINTER(ctypes.c_float)]),
     ]:
         f = getattr(B, name)
         f.restype, f.argtypes = res, args
@@ -399,6 +400,32 @@ def run_i8(args, K, B):
     return lines
 
 
+def run_bi(args, K, B):
+    """The batch-invariant bf16 GEMV (ak_bf16_gemv_bi; reference bi_gemv.cu): a 5120 x 5120 bf16 weight (weights
+    rotated over >= 1 GB of copies) and a small-n projection (48 x 5120), M = 1, 16, 128."""
+    ctx = Ctx(K, B)
+    lines = []
+    for n, k in ((5120, 5120), (48, 5120)):
+        one = n * k * 2
+        copies = max(2, (1 << 30) // one + 1)
+        w = ctx.alloc(copies * one)
+        ctx.check(B.agb_gen_x(SEED + 41, copies * n * k, 0.02, w, None), "gen w")
+        for m in (1, 16, 128):
+            x, y = ctx.alloc(m * k * 2), ctx.alloc(m * n * 2)
+            ctx.check(B.agb_gen_x(SEED + 42, m * k, 1.0, x, None), "gen x")
+            t = ctypes.c_float()
+            ctx.check(B.agb_time_bi_gemv(x, w, y, m, n, k, copies, args.warmup, max(args.steps, 20), ctypes.byref(t)),
+                      "bi gemv")
+            us = t.value * 1e3
+            by = n * k * 2 + m * k * 2 + m * n * 2
+            lines.append({"config": "bf16_gemv_bi", "n": n, "k": k, "m": m, "us": round(us, 2),
+                          "GBps": round(by / (us * 1e-6) / 1e9, 1),
+                          "pct_of_peak": round(100 * by / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 2),
+                          "TFLOPs": round(2.0 * m * n * k / (us * 1e-6) / 1e12, 2), "copies": copies, "graph": True})
+        ctx.free_all()
+    return lines
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -431,6 +458,9 @@ def main():
             raise RuntimeError("calibration copy failed")
     if args.config == "sweep":
         print(json.dumps(run_sweep(args, K, B)), flush=True)
+    elif args.config == "bi":
+        for line in run_bi(args, K, B):
+            print(json.dumps(line), flush=True)
     elif args.config == "i8":
         for line in run_i8(args, K, B):
             print(json.dumps(line), flush=True)
