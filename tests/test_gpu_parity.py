@@ -326,3 +326,31 @@ def test_multi_segment_small_m_oracle(bits, m, k):
             if rows:
                 got, want = got[:, :64], want[:, :64]
             assert (got == want).all(), f"segment {i}"
+
+
+def test_exact_order_known_answers_on_gpu():
+    """The hand-computed order cases of the oracle tests (EXACT_ORDER_CASES): the GPU exact path gives the reference's
+    values, where other summation orders give others; the default numerics give the oracle's (their group sums are
+    exact sums of 22-bit fixed-point activations relative to the group's largest: next to 2^24, a 1.0 truncates to 0)."""
+    from test_oracle import EXACT_ORDER_CASES
+    K = kernels()
+    k = 4096
+    packed = np.full(k // 8, 0x99999999, dtype=np.uint32)  # q = 1
+    scales = np.full(k // 128, 0x3F80, dtype=np.uint16)     # 1.0
+    L = Linear(packed, scales, 1, k, 128, 4)
+    check(L.rc, "repack")
+    for vals, want in EXACT_ORDER_CASES:
+        xf = np.zeros(k, dtype=np.float32)
+        for i, v in vals.items():
+            xf[i] = v
+        X = Dev.of(f2bf_array(xf))
+        K.ak_w4_set_mma(0)
+        try:
+            for bw in (0, 1):
+                (Y,) = gemv(4, X, 1, [L], k, 128, bf16w=bw)
+                assert bf2f_array(Y.get(np.uint16, 1))[0] == want, (vals, bw)
+        finally:
+            K.ak_w4_set_mma(1)
+        (Y,) = gemv(4, X, 1, [L], k, 128)
+        wt, st = L.host_kt()
+        assert np.array_equal(Y.get(np.uint16, 1), ora_fast(4, f2bf_array(xf), 1, wt, st, 1, k, 128).reshape(-1))

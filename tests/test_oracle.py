@@ -304,3 +304,41 @@ def test_i8_gemv_within_fp64_bound():
     mag = (np.abs(xf) @ np.abs(q.astype(np.float64)).T) * scale[None, :]
     # bf16 output rounding (2^-9 relative) plus fp32 summation error (k * 2^-24 of sum |x q|)
     assert np.all(np.abs(y - ref) <= np.abs(ref) * 2.0 ** -8 + mag * k * 2.0 ** -24)
+
+
+# ------------------------------------------------------------------------------------------------ exact path order
+def exact_order_case(vals, k=4096):
+    """One W4 row of q = 1 (container nibbles 9), scales 1.0, group 128; x zero but for `vals` {input: value}."""
+    n = 1
+    packed = np.full(n * k // 8, 0x99999999, dtype=np.uint32)
+    scales = np.full(n * k // 128, 0x3F80, dtype=np.uint16)
+    rc, wt, st = ora_repack(4, packed, scales, n, k, 128)
+    assert rc == 0
+    xf = np.zeros(k, dtype=np.float32)
+    for i, v in vals.items():
+        xf[i] = v
+    return f2bf_array(xf), wt, st
+
+
+# Hand-computed answers where the reference's exact order (w4_gemv.cu:117-127, 279-349: per lane chunk four 8-input fma
+# chains from 0 added left to right, acc = fma(d, s, acc) over the lane's tiles in order, xor butterfly 16..1 over the
+# 32 lanes) differs from other orders.  Input i: tile i // 1024, lane (i % 1024) // 32, chunk word (i % 32) // 8.
+EXACT_ORDER_CASES = [
+    # one 8-input chain: 2^24, +1 (lost), +1 (lost), -2^24 -> 0 (a pairwise sum gives 1)
+    ({0: 2.0 ** 24, 1: 1.0, 2: 1.0, 3: -(2.0 ** 24)}, 0.0),
+    # the chunk's four chains added left to right: ((2^24 + 1) + 1) - 2^24 = 0 (pairwise: 1)
+    ({0: 2.0 ** 24, 8: 1.0, 16: 1.0, 24: -(2.0 ** 24)}, 0.0),
+    # one lane over its tiles, acc = fma(d, s, acc) in tile order: 0 (pairwise over tiles: 1)
+    ({0: 2.0 ** 24, 1024: 1.0, 2048: 1.0, 3072: -(2.0 ** 24)}, 0.0),
+    # lanes 0..3 of one tile through the butterfly: (l0 + l2) + (l1 + l3) = 0 + 2 (left to right: 1)
+    ({0: 2.0 ** 24, 32: 1.0, 64: -(2.0 ** 24), 96: 1.0}, 2.0),
+]
+
+
+@pytest.mark.parametrize("case", range(len(EXACT_ORDER_CASES)))
+@pytest.mark.parametrize("bf16w", [0, 1])
+def test_exact_order_known_answers(case, bf16w):
+    vals, want = EXACT_ORDER_CASES[case]
+    x, wt, st = exact_order_case(vals)
+    y = ora_exact(4, x, 1, wt, st, 1, 4096, 128, bf16w=bf16w)
+    assert bf2f_array(y.reshape(-1))[0] == want
