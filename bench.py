@@ -155,9 +155,12 @@ def layer_bits(layer):
     return 2 if u < 0.3 else (3 if u < 0.8 else 4)
 
 
-def build_sweep(ctx, m, cpu_layers):
-    """64 layers + LM head; returns (plan, meta, containers for the CPU baseline)."""
+def build_sweep(ctx, m, cpu_layers, tp=1):
+    """64 layers + LM head; returns (plan, meta, containers for the CPU baseline).  tp > 1: one rank's shard of a
+    tensor-parallel layer (m1.rs:58-77 tp_rule): q/k/v, gate_up and the LM head by output rows (n / tp), o and down by
+    k (k / tp; the all-reduce of their outputs is not part of this one-GPU build)."""
     H, KV, INTER, VOCAB = 5120, 1024, 27648, 152064
+    T = tp
     B = ctx.B
     # staging for the containers (largest: LM head 152064 x 5120)
     ct = ctx.alloc(VOCAB * H // 2, keep=False)
@@ -174,18 +177,18 @@ def build_sweep(ctx, m, cpu_layers):
         b = layer_bits(l)
         s = SEED * 1000 + 10 * l
         keep = l < cpu_layers
-        q = QLinear(ctx, s + 0, H, H, b, ct=ct, cs=cs, keep_container=keep)
-        kk = QLinear(ctx, s + 2, KV, H, b, ct=ct, cs=cs, keep_container=keep)
-        v = QLinear(ctx, s + 4, KV, H, b, ct=ct, cs=cs, keep_container=keep)
-        o = QLinear(ctx, s + 6, H, H, b, ct=ct, cs=cs, keep_container=keep)
-        gu = QLinear(ctx, s + 8, 2 * INTER, H, b, ct=ct, cs=cs, keep_container=keep)
-        dn = QLinear(ctx, s + 10, H, INTER, b, ct=ct, cs=cs, keep_container=keep)
-        plan += [launch(b, m, H, xh, [q, kk, v], [yq, yk, yv]), launch(b, m, H, xh, [o], [yo]),
-                 launch(b, m, H, xh, [gu], [yg]), launch(b, m, INTER, xd, [dn], [ydn])]
+        q = QLinear(ctx, s + 0, H // T, H, b, ct=ct, cs=cs, keep_container=keep)
+        kk = QLinear(ctx, s + 2, KV // T, H, b, ct=ct, cs=cs, keep_container=keep)
+        v = QLinear(ctx, s + 4, KV // T, H, b, ct=ct, cs=cs, keep_container=keep)
+        o = QLinear(ctx, s + 6, H, H // T, b, ct=ct, cs=cs, keep_container=keep)
+        gu = QLinear(ctx, s + 8, 2 * INTER // T, H, b, ct=ct, cs=cs, keep_container=keep)
+        dn = QLinear(ctx, s + 10, H, INTER // T, b, ct=ct, cs=cs, keep_container=keep)
+        plan += [launch(b, m, H, xh, [q, kk, v], [yq, yk, yv]), launch(b, m, H // T, xh, [o], [yo]),
+                 launch(b, m, H, xh, [gu], [yg]), launch(b, m, INTER // T, xd, [dn], [ydn])]
         meta += [("qkv", b), ("o", b), ("gate_up", b), ("down", b)]
         if keep:
-            cpu += [(xh, H, [q, kk, v]), (xh, H, [o]), (xh, H, [gu]), (xd, INTER, [dn])]
-    lm = QLinear(ctx, SEED * 1000 + 999, VOCAB, H, 4, ct=ct, cs=cs)
+            cpu += [(xh, H, [q, kk, v]), (xh, H // T, [o]), (xh, H, [gu]), (xd, INTER // T, [dn])]
+    lm = QLinear(ctx, SEED * 1000 + 999, VOCAB // T, H, 4, ct=ct, cs=cs)
     plan.append(launch(4, m, H, xh, [lm], [ylm]))
     meta.append(("lm_head", 4))
     ctx.check(ctx.K.ak_synchronize(), "sync")
@@ -252,7 +255,7 @@ def run_sweep(args, K, B):
     ctx = Ctx(K, B)
     cpu_layers = 0 if args.no_cpu else 24  # containers kept on the host for the CPU baseline (about 20 s of it)
     t0 = time.time()
-    plan, meta, cpu = build_sweep(ctx, args.m, cpu_layers)
+    plan, meta, cpu = build_sweep(ctx, args.m, cpu_layers, args.tp)
     print(f"# sweep generated in {time.time() - t0:.1f} s ({len(plan)} launches)", file=sys.stderr, flush=True)
     arr = (AgbLaunch * len(plan))(*plan)
     total_bytes = sum(algo_bytes(L) for L in plan)
@@ -291,14 +294,14 @@ def run_sweep(args, K, B):
     bits_mix = {f"w{b}": sum(1 for (_, bb) in meta[:-1] if bb == b) // 4 for b in (2, 3, 4)}
     traffic = None
     tf = os.path.join(ROOT, "profiles", "traffic.json")  # HBM bytes per launch from rocprofv3 FETCH_SIZE / WRITE_SIZE
-    if args.m == 1 and os.path.exists(tf):
+    if args.m == 1 and args.tp == 1 and os.path.exists(tf):
         try:
             traffic = json.load(open(tf)).get(dom_name, {}).get("bytes_per_launch")
         except (OSError, ValueError):
             traffic = None
     if use_chain:  # the dominant (only) kernel is the chained launch: one dispatch per sweep
         ctraffic = None
-        if args.m == 1 and os.path.exists(tf):
+        if args.m == 1 and args.tp == 1 and os.path.exists(tf):
             try:
                 ctraffic = json.load(open(tf)).get("chain_sweep", {}).get("bytes_per_launch")
             except (OSError, ValueError):
@@ -322,7 +325,7 @@ def run_sweep(args, K, B):
                                "gate_up 5120->55296, down 27648->5120, mixed W2/W3/W4 g128 per layer, "
                                "+ W4 LM head 5120->152064",
                    "m": args.m, "layers_by_bits": bits_mix, "launches": len(plan),
-                   "bytes_per_sweep": total_bytes, "graph": not args.eager, "parallelism": "single GPU",
+                   "bytes_per_sweep": total_bytes, "graph": not args.eager, "parallelism": "single GPU" if args.tp == 1 else f"one rank of tp{args.tp}: per-rank shapes, no all-reduce",
                    "chained": use_chain},
         "roofline": roof,
         "one_launch_per_linear": {"us_per_sweep": round(ms_l.value * 1e3, 1),
@@ -432,6 +435,8 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--m", type=int, default=1)
+    ap.add_argument("--tp", type=int, default=1, choices=[1, 2, 4, 8],
+                    help="sweep over one rank's shard of a tensor-parallel decode layer (not the headline)")
     ap.add_argument("--config", default="sweep")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true")
