@@ -414,4 +414,42 @@ int agb_copy(size_t bytes, int reps) {
   return e;
 }
 
+// The GEMV-versus-GEMM crossover: `steps` eager calls on one stream after `warmup`, weights rotated over `ncopies`
+// KT copies (wts[c], sts[c]); *ms = the mean time per call (HIP events).
+//   mode 0: ak_wq_gemv_kt_multi (the quantized GEMV, m <= 128);
+//   mode 1: ak_wq_dequant_kt_rows of all n rows into wdense, then ak_bf16_linear_f32reduce (the prefill route).
+int agb_time_xover(int bits, const void* x, int m, const void* const* wts, const void* const* sts, int ncopies,
+                   void* wdense, void* y, int n, int k, int mode, int warmup, int steps, float* ms) {
+  hipStream_t s;
+  int e = (int)hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+  if (e) return e;
+  auto one = [&](int i) {
+    const void* w = wts[i % ncopies];
+    const void* sc = sts[i % ncopies];
+    if (mode == 0) {
+      void* yy = y;
+      return ak_wq_gemv_kt_multi(bits, x, m, 1, &w, &sc, &yy, &n, nullptr, k, 128, 0, s);
+    }
+    int r = ak_wq_dequant_kt_rows(bits, w, sc, wdense, n, k, 128, 0, n, s);
+    if (!r) r = ak_bf16_linear_f32reduce(x, wdense, y, m, n, k, s);
+    return r;
+  };
+  for (int i = 0; i < warmup && !e; ++i) e = one(i);
+  hipEvent_t a, b;
+  hipEventCreate(&a);
+  hipEventCreate(&b);
+  if (!e) e = (int)hipEventRecord(a, s);
+  for (int i = 0; i < steps && !e; ++i) e = one(i);
+  if (!e) e = (int)hipEventRecord(b, s);
+  if (!e) e = (int)hipEventSynchronize(b);
+  float t = 0.f;
+  if (!e) e = (int)hipEventElapsedTime(&t, a, b);
+  *ms = t / steps;
+  hipEventDestroy(a);
+  hipEventDestroy(b);
+  hipStreamSynchronize(s);
+  hipStreamDestroy(s);
+  return e;
+}
+
 }  // extern "C"

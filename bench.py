@@ -10,7 +10,7 @@ reference's int4 container and repacked by ak_wq_repack_kt; inputs are resident 
 
 Effective bytes per launch = packed weights + bf16 scales + bf16 x + bf16 y (the algorithmic bytes).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--m 1] [--config sweep|0|1|2|3|i8|bi] [--no-cpu] [--eager]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--m 1] [--config sweep|0|1|2|3|i8|bi|xover] [--no-cpu] [--eager]
 """
 import argparse
 import ctypes
@@ -403,6 +403,48 @@ def run_i8(args, K, B):
     return lines
 
 
+def run_xover(args, K, B):
+    """The GEMV-versus-GEMM crossover in M: the quantized GEMV (ak_wq_gemv_kt_multi, M <= 128) against the prefill
+    route (ak_wq_dequant_kt_rows of the whole weight, then the bf16 library GEMM ak_bf16_linear_f32reduce; the
+    reference's route above 128 tokens, m1_model.cu:1876-1897) on gate_up W3 (55296 x 5120), o W4 (5120 x 5120) and
+    down W2 (5120 x 27648); weights rotated over copies beyond the 256 MB cache.  Eager calls, HIP events."""
+    ctx = Ctx(K, B)
+    vp = ctypes.c_void_p
+    B.agb_time_xover.argtypes = [ctypes.c_int, vp, ctypes.c_int, ctypes.POINTER(vp), ctypes.POINTER(vp), ctypes.c_int,
+                                 vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                 ctypes.POINTER(ctypes.c_float)]
+    B.agb_time_xover.restype = ctypes.c_int
+    ms_list = [1, 2, 4, 8, 16, 32, 64, 128, 256, 512]
+    lines = []
+    for name, bits, n, k in (("gate_up_w3", 3, 55296, 5120), ("o_w4", 4, 5120, 5120), ("down_w2", 2, 5120, 27648)):
+        lins = []
+        while sum(L.wbytes for L in lins) < 400e6:
+            lins.append(QLinear(ctx, SEED * 1000 + 700 + len(lins), n, k, bits))
+        wts = (vp * len(lins))(*[L.wt for L in lins])
+        sts = (vp * len(lins))(*[L.st for L in lins])
+        mmax = ms_list[-1]
+        x = ctx.alloc(mmax * k * 2)
+        y = ctx.alloc(mmax * n * 2)
+        wd = ctx.alloc(n * k * 2)
+        ctx.check(B.agb_gen_x(SEED + 41, mmax * k, 1.0, x, None), "gen x")
+        row = {"config": "xover", "linear": name, "bits": bits, "n": n, "k": k, "copies": len(lins),
+               "us_gemv": {}, "us_dequant_gemm": {}}
+        for m in ms_list:
+            t = ctypes.c_float()
+            if m <= 128:
+                ctx.check(B.agb_time_xover(bits, x, m, wts, sts, len(lins), wd, y, n, k, 0, 3, 20, ctypes.byref(t)),
+                          "gemv")
+                row["us_gemv"][m] = round(t.value * 1e3, 2)
+            ctx.check(B.agb_time_xover(bits, x, m, wts, sts, len(lins), wd, y, n, k, 1, 2, 10, ctypes.byref(t)),
+                      "dequant + gemm")
+            row["us_dequant_gemm"][m] = round(t.value * 1e3, 2)
+        faster = [m for m in row["us_gemv"] if row["us_dequant_gemm"][m] < row["us_gemv"][m]]
+        row["crossover_m"] = min(faster) if faster else None
+        lines.append(row)
+        ctx.free_all()
+    return lines
+
+
 def run_bi(args, K, B):
     """The batch-invariant bf16 GEMV (ak_bf16_gemv_bi; reference bi_gemv.cu): a 5120 x 5120 bf16 weight (weights
     rotated over >= 1 GB of copies) and a small-n projection (48 x 5120), M = 1, 16, 128."""
@@ -465,6 +507,9 @@ def main():
         print(json.dumps(run_sweep(args, K, B)), flush=True)
     elif args.config == "bi":
         for line in run_bi(args, K, B):
+            print(json.dumps(line), flush=True)
+    elif args.config == "xover":
+        for line in run_xover(args, K, B):
             print(json.dumps(line), flush=True)
     elif args.config == "i8":
         for line in run_i8(args, K, B):
