@@ -247,3 +247,46 @@ def test_chain_independent_step_after_a_step_most_workgroups_skip():
         check(K.ak_synchronize(), "sync")
         for g, (y, n, name) in zip(got, ((y1, 27648, "A"), (y2, 16, "B"), (y3, 4096, "C"))):
             assert np.array_equal(g, y.get(np.uint16, n)), f"run {rep} step {name}"
+
+
+def build_rank(m, layers, tp, H=5120, KV=1024, INTER=27648):
+    """Steps of one tensor-parallel rank's decoder layers: qkv (rows / tp, x = h) -> o (k = H / tp, x = the rank's q
+    rows) -> gate_up (rows / tp, x = o) -> down (k = INTER / tp, x = the first INTER / tp gate_up rows) -> h."""
+    h = Dev(m * H * 2)
+    steps, flow = [], []
+    x = h
+    for li, bits in enumerate(layers):
+        s = 3000 + 37 * li
+        q, kk, v = Lin(s, H // tp, H, bits), Lin(s + 2, KV // tp, H, bits), Lin(s + 4, KV // tp, H, bits)
+        o, gu, dn = Lin(s + 6, H, H // tp, bits), Lin(s + 8, 2 * INTER // tp, H, bits), Lin(s + 10, H, INTER // tp, bits)
+        yq, yk, yv = Dev(m * H // tp * 2), Dev(m * KV // tp * 2), Dev(m * KV // tp * 2)
+        yo, ygu, yh = Dev(m * H * 2), Dev(m * 2 * INTER // tp * 2), Dev(m * H * 2)
+        for lins, xin, k, ys in [([q, kk, v], x, H, [yq, yk, yv]), ([o], yq, H // tp, [yo]), ([gu], yo, H, [ygu]),
+                                 ([dn], ygu, INTER // tp, [yh])]:
+            steps.append(wq_step(bits, xin, m, [l.L for l in lins], ys, k))
+            flow.append((lins, xin, k, ys))
+        x = yh
+    return h, steps, flow
+
+
+@pytest.mark.parametrize("m", [1, 2])
+def test_chain_at_tp8_rank_shapes_matches_oracle(m):
+    """One TP = 8 rank's layers in one chained launch (o at k = 640: one padded tile; down at k = 3456: the last of
+    four tiles padded; the down steps split k across workgroups): every step's outputs equal the oracle applied step
+    by step, and equal one launch per step."""
+    K = kernels()
+    h, steps, flow = build_rank(m, [3, 2, 4], 8)
+    ch = Chain(steps)
+    assert ch.chained
+    h_host = gen_x(5150 + m, m * 5120)
+    check(K.ak_memcpy_h2d(h.p, h_host.ctypes.data, h_host.nbytes), "h2d")
+    want = oracle_flow(h_host, m, flow)
+    ch.run()
+    check(K.ak_synchronize(), "sync")
+    assert K.ak_wq_chain_status() == 0
+    assert_same(read_outputs(m, flow), want, "chain vs oracle")
+    zero_outputs(flow)
+    for lins, xin, k, ys in flow:
+        gemv(lins[0].bits, xin.p, m, [l.L for l in lins], k, 128, ys=ys)
+    check(K.ak_synchronize(), "sync")
+    assert_same(read_outputs(m, flow), want, "launches vs oracle")
