@@ -492,10 +492,11 @@ int mt_chunk_groups(int nquad, int P, int nch) {
   return cg;
 }
 
-// split-K for activations beyond the LDS up to this many 16-row blocks per CU (above it the partials' traffic costs
-// more than the chunked launch's repeated passes)
+// split-K for activations beyond the LDS up to this many 16-row blocks per CU.  Measured at 16 tokens, k = 5120:
+// gate_up (13.5 blocks per CU) 55-64 -> 44-57 us and the 152064-row LM head (37 per CU, two 8-token launches before)
+// 167 -> 145 us against the chunked launch; the stripe partials (P x tokens x rows x 4 B) stay well below the weights.
 #ifndef AK_MT_SK_BLOCKS
-#define AK_MT_SK_BLOCKS 8
+#define AK_MT_SK_BLOCKS 40
 #endif
 template <int BITS, int NT>
 int launch_mt(I8Args a, hipStream_t s) {
