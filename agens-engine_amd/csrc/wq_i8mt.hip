@@ -103,14 +103,23 @@ __host__ __device__ inline int mt_meta_bytes(int ngroups, int nt) { return nt * 
 // rows of range r, converting only that stripe's activations; it writes its stripe partials with device-coherent
 // stores, and the last of the range's P workgroups (device-scope counter) adds them in stripe order and writes y.
 // ACT (split-K launches only): x is the merged gate_up [m][2k], the activations SiLU(gate) * up (ak_silu_mul's value)
-template <int BITS, int SPLIT, int DEPTH, int NT, bool CH, bool SK = false, bool ACT = false>
+//
+// TH (split-K only, one segment, 9..16 tokens as NT = 2): the launch holds two token halves, workgroups [0, W) for
+// tokens 0..7 and [W, 2W) for tokens 8.. (W = a.wg_end[3]); each half computes exactly what the 8-token launch of its
+// tokens computes, with its own stripe partials and counters.
+template <int BITS, int SPLIT, int DEPTH, int NT, bool CH, bool SK = false, bool ACT = false, bool TH = false>
 __global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
+  static_assert(!TH || (SK && NT == 2), "token halves: split-K launches of 8-token halves");
   static_assert((!CH && !SK) || SPLIT == 1, "chunked and split launches give every wave whole stripes of its blocks");
   static_assert(!(CH && SK), "one of the two");
   extern __shared__ __attribute__((aligned(256))) uint8_t lds[];
   constexpr int LPU = kG / 8, UPW = 64 / LPU, XB = 4, MP = 4 * NT;  // MP: padded tokens
   constexpr int REC = 128 * BITS;
-  const int P = a.P, nquad = a.nquad, k = a.k, mm = a.m;
+  const int P = a.P, nquad = a.nquad, k = a.k;
+  const int thw = TH ? a.wg_end[kMaxSegs - 1] : 0, th = TH && (int)blockIdx.x >= thw ? 1 : 0;
+  const int bid = (int)blockIdx.x - th * thw;  // the workgroup's index within its token half
+  const int mm = TH ? (th ? a.m - 8 : 8) : a.m;
+  const uint16_t* const xb = a.x + (TH ? (size_t)th * 8 * (ACT ? 2 * k : k) : 0);
   const int ngroups = nquad * 4;
   const int nwv = blockDim.x >> 6;
   const int tid = threadIdx.x;
@@ -120,20 +129,20 @@ __global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
   // this workgroup's segment and its 16-row blocks [b_lo, b_lo + nb) of that segment (SK: row range r, stripe psk)
   int sg = 0;
 #pragma unroll
-  for (int i = 1; i < kMaxSegs; ++i) sg += (i < sgs.nseg && (int)blockIdx.x >= a.wg_end[i - 1]) ? 1 : 0;
+  for (int i = 1; i < kMaxSegs; ++i) sg += (i < sgs.nseg && bid >= a.wg_end[i - 1]) ? 1 : 0;
   // (SK: segment i has (wg_end[i] - wg_end[i-1]) / P row ranges; range r of the segment is counter wg0 / P + r, its
   // partials start after the earlier segments')
-  const int wg0 = sg ? AK_PICK(sg - 1, a.wg_end) : 0, li = (int)blockIdx.x - wg0;
+  const int wg0 = sg ? AK_PICK(sg - 1, a.wg_end) : 0, li = bid - wg0;
   const int nr = SK ? (AK_PICK(sg, a.wg_end) - wg0) / P : 1, r = SK ? li / P : 0, psk = SK ? li - r * P : 0;
   const int gs = SK ? nr : AK_PICK(sg, a.wg_end) - wg0, w = SK ? r : li;
   const int n = AK_PICK(sg, sgs.n), n_b16 = (n + 15) >> 4;
   // 32-bit divisions (w < 1024 workgroups, < 2^21 blocks): a 64-bit one is a long instruction sequence on the GPU
   const int b_lo = (int)((unsigned)w * (unsigned)n_b16 / (unsigned)gs);
   const int nb = (int)((unsigned)(w + 1) * (unsigned)n_b16 / (unsigned)gs) - b_lo;
-  uint16_t* const yseg = AK_PICK(sg, sgs.y);
   const int ldy = AK_PICK(sg, sgs.ldy);
-  float* spart = a.part;
-  int* scnt = a.cnt;
+  uint16_t* const yseg = AK_PICK(sg, sgs.y) + (TH ? (size_t)th * 8 * ldy : 0);
+  float* spart = a.part + (TH ? (size_t)th * P * MP * n_b16 * 16 : 0);
+  int* scnt = a.cnt + (TH ? th * (thw / P) : 0);
   if constexpr (SK) {
 #pragma unroll
     for (int i = 0; i < kMaxSegs - 1; ++i)
@@ -193,8 +202,8 @@ __global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
       xv[b] = make_uint4(0u, 0u, 0u, 0u);
       if (pass0 + b < npass) {
         const size_t xo = ok ? (size_t)t * (ACT ? 2 * k : k) + kk : 0;
-        uint4 v = *reinterpret_cast<const uint4*>(a.x + xo);
-        if constexpr (ACT) v = silu_mul8(v, *reinterpret_cast<const uint4*>(a.x + xo + k));
+        uint4 v = *reinterpret_cast<const uint4*>(xb + xo);
+        if constexpr (ACT) v = silu_mul8(v, *reinterpret_cast<const uint4*>(xb + xo + k));
         xv[b] = ok ? v : make_uint4(0u, 0u, 0u, 0u);
       }
     }
@@ -476,10 +485,10 @@ size_t mt_block_bytes(int P, int split, int nt) {  // per 16-row block: outputs,
   return (size_t)4 * nt * 16 * 2 + (split > 1 ? (size_t)P * 4 * nt * 16 * 4 + 4 : 0);
 }
 
-template <int BITS, int SPLIT, int NT, bool CH, bool SK = false, bool ACT = false>
+template <int BITS, int SPLIT, int NT, bool CH, bool SK = false, bool ACT = false, bool TH = false>
 void launch_mt_split(const I8Args& a, int grid, size_t smem, hipStream_t s) {
   constexpr int DEPTH = NT > 2 ? 1 : 2;  // items in flight per wave (16 tokens: their accumulators take the registers)
-  hipLaunchKernelGGL((i8_mt_kernel<BITS, SPLIT, DEPTH, NT, CH, SK, ACT>), dim3(grid), dim3(1024), smem, s, a);
+  hipLaunchKernelGGL((i8_mt_kernel<BITS, SPLIT, DEPTH, NT, CH, SK, ACT, TH>), dim3(grid), dim3(1024), smem, s, a);
 }
 
 // groups of the largest of nch chunks of stripes
@@ -554,6 +563,31 @@ int launch_mt(I8Args a, hipStream_t s) {
       else
         launch_mt_split<BITS, 1, NT, false, true>(b, b.wg_end[g.nseg - 1], smem, s);
       return (int)hipGetLastError();
+    }
+    // 9..16 tokens, one segment, one stripe's 16-token image beyond the LDS: both 8-token halves in one split-K
+    // launch (NT = 2 each, the same results as two 8-token launches).  Half the row ranges per half keep the grid at
+    // one workgroup per CU, and the two halves of a (range, stripe) run at once on the same XCD (workgroups 128 apart),
+    // so the second one's weights come from the L2: down 5120 x 27648 at 16 tokens, W2 / W3 / W4 44.8 / 59.6 / 54.4 ->
+    // 30.4 / 42.9 / 40.7 us (full ranges per half, two rounds of workgroups: 43.3 / 57.1 / 52.5 us).
+    if constexpr (NT == 4) {
+      const int nrh = nrt / 2 > 0 ? nrt / 2 : 1;  // row ranges per half
+      const int nbs = (g.n[0] + 15) / 16, nbr2 = (nbs + nrh - 1) / nrh;
+      const size_t smem2 = 256 + (size_t)mt_a_bytes(cg, 2) + mt_meta_bytes(cg, 2) + (size_t)nbr2 * 4 * 2 * 16 * 2 + 16;
+      const size_t pf = (size_t)a.P * 4 * 2 * nbs * 16;  // one half's stripe partials (floats)
+      if (g.nseg == 1 && a.m > 8 && 2 * nrh <= 1024 && smem2 <= 160 * 1024) {
+        void* z2 = stream_scratch(s, 4096 + 2 * pf * 4);
+        if (z2) {
+          I8Args b = a;
+          for (int i = 0; i < kMaxSegs; ++i) b.wg_end[i] = nrh * a.P;
+          b.cnt = static_cast<int*>(z2);
+          b.part = reinterpret_cast<float*>(static_cast<uint8_t*>(z2) + 4096);
+          if (a.act)
+            launch_mt_split<BITS, 1, 2, false, true, true, true>(b, 2 * nrh * a.P, smem2, s);
+          else
+            launch_mt_split<BITS, 1, 2, false, true, false, true>(b, 2 * nrh * a.P, smem2, s);
+          return (int)hipGetLastError();
+        }
+      }
     }
   }
   if (a.act) return AK_INVALID;  // the SiLU(gate) * up activation: split-K launches only (the caller falls back)

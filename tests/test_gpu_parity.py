@@ -354,3 +354,23 @@ def test_exact_order_known_answers_on_gpu():
         (Y,) = gemv(4, X, 1, [L], k, 128)
         wt, st = L.host_kt()
         assert np.array_equal(Y.get(np.uint16, 1), ora_fast(4, f2bf_array(xf), 1, wt, st, 1, k, 128).reshape(-1))
+
+
+@pytest.mark.parametrize("bits", [4, 3, 2])
+@pytest.mark.parametrize("m", [9, 12, 16])
+def test_long_k_nine_to_sixteen_tokens(bits, m):
+    """9..16 tokens at k = 27648, one segment (one stripe's 16-token activation image exceeds the LDS): rows equal
+    the oracle, the 8-token launches of the same tokens, and a second launch (the split's counters return to zero)."""
+    k, g, n = 27648, 128, 900
+    A = make_linear(1970 + bits, n, k, g, bits)
+    x = gen_x(1990 + m, m * k)
+    X = Dev.of(x)
+    y1 = y_of(gemv(bits, X, m, [A], k, g)[0], m, n)
+    assert np.array_equal(y1, y_of(gemv(bits, X, m, [A], k, g)[0], m, n))
+    lo = y_of(gemv(bits, X, 8, [A], k, g)[0], 8, n)
+    hi = y_of(gemv(bits, X.addr(8 * k * 2), m - 8, [A], k, g)[0], m - 8, n)
+    assert np.array_equal(y1[:8], lo) and np.array_equal(y1[8:], hi)
+    wt, st = A.host_kt()
+    for r0 in (0, 448, n - 40):
+        yo = ora_fast(bits, x, m, wt, st, n, k, g, rows=(r0, r0 + 40))
+        assert (y1[:, r0:r0 + 40] == yo[:, r0:r0 + 40]).all(), f"rows {r0}"
