@@ -122,8 +122,9 @@ __global__ void __launch_bounds__(kWaves * 64) bi_gemv_kernel(const uint16_t* __
 
 extern "C" int ak_bf16_gemv_bi_ld(const void* x, const void* w, const void* bias, void* y, int m, int n, int k, long ldy,
                                   void* stream) {
-  // the reference's checks (bi_gemv.cu:276), and null pointers / empty shapes
-  if (!x || !w || !y || m < 1 || m > 128 || n < 1 || k < 32 || k % 32 != 0) return AK_INVALID;
+  // the reference's checks (bi_gemv.cu:276), null pointers / empty shapes, and a row stride below n (token rows would
+  // overlap)
+  if (!x || !w || !y || m < 1 || m > 128 || n < 1 || k < 32 || k % 32 != 0 || ldy < n) return AK_INVALID;
   hipStream_t s = static_cast<hipStream_t>(stream);
   auto X = static_cast<const uint16_t*>(x);
   auto W = static_cast<const uint16_t*>(w);

@@ -43,7 +43,7 @@ namespace {
 
 // LDS layout of a stripe-wave's activation batch:
 //   xl[(((qi * CPQ + cq) * 2 + half) * m + token) * 48 + limb * 16 + 4v + b]   (three 16-byte limb rows per token)
-//   ex[(qi * 4 + gq) * m + token] = E
+//   ex[(qi * 4 + gq) * m + token] = the group's largest bf16 magnitude pattern (act_scale_bits' argument)
 // Converts the units (quad qi, group gq, token j) of quads stripe_begin(p) + i0 + qi, qi < nbq; the RW waves of this stripe
 // share the work: the LPU = G / 8 lanes of a unit hold 8 consecutive inputs each.
 template <int BITS, int G, int RW>

@@ -127,8 +127,25 @@ __device__ __forceinline__ float group_sum_f32(const i32x4& d) {
   return fmaf((float)t, 256.0f, (float)d[0]);
 }
 
-// 2^(E - 148) as fp32 bits (the activation scale of a group whose largest exponent field is E)
-__device__ __forceinline__ int act_scale_bits(int e) { return __float_as_int(ldexpf(1.0f, e - 148)); }
+// The activation scale of a group as fp32 bits, from the group's largest bf16 magnitude pattern mx (sign cleared):
+// 2^(E - 148) with E = mx >> 7 the largest exponent field; a group holding a NaN (mx above the Inf pattern 0x7F80):
+// NaN; a group holding an Inf but no NaN: +Inf.  In a non-finite group every finite input converts to 0 and every Inf
+// to its sign (+-1, see clamp_nonfinite), so the group sum S is the sum of sign(x) * q over the Inf inputs and the
+// group adds S * scale * Inf: +-Inf, or NaN where S = 0 -- the fp32 path's value wherever the group's Inf products
+// share one sign (the fp32 path gives NaN for products of both signs, where S may be nonzero).
+__device__ __forceinline__ int act_scale_bits(int mx) {
+  return mx > 0x7F80 ? 0x7FC00000 : mx == 0x7F80 ? 0x7F800000 : __float_as_int(ldexpf(1.0f, (mx >> 7) - 148));
+}
+
+// x_int of a non-finite group (E = 255): trunc(x * 2^-107) is 0 for every finite bf16, the conversion saturates for
+// +-Inf and gives 0 for NaN; clamped to [-1, 1] that is sign(x) for an Inf and 0 otherwise.  A finite group is left
+// as it is (the branch is skipped when no lane of the wave holds a non-finite group).
+__device__ __forceinline__ void clamp_nonfinite(int e, int (&xi)[8]) {
+  if (e == 255) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xi[i] = min(max(xi[i], -1), 1);
+  }
+}
 
 // Reductions over aligned groups of L lanes (L = 2, 4, 8 or 16) with DPP: two quad swaps, then the half-row and the
 // row mirrors (each step pairs every lane with one holding the other half of its group's partial results).
@@ -155,23 +172,30 @@ __device__ __forceinline__ int limb_sum8(const uint32_t (&t)[8], int j) {
 }
 
 // One group's activation limbs from 8 consecutive bf16 inputs per lane, LPU lanes per group: the group's largest
-// exponent field e (all LPU lanes) and, per input, x_int = trunc(x * 2^(148 - e)) with its three limb-byte sources.
+// magnitude pattern mx (all LPU lanes; the exponent field E = mx >> 7) and, per input, x_int = trunc(x * 2^(148 - E))
+// with its three limb-byte sources.
 template <int LPU>
 __device__ __forceinline__ int group_limbs(const uint4 v, uint32_t (&t0)[8], uint32_t (&t1)[8], uint32_t (&t2)[8]) {
   const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-  int e = 0;
+  int mx = 0;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) e = max(e, max((int)((w[i] >> 7) & 0xFFu), (int)((w[i] >> 23) & 0xFFu)));
-  e = dpp_group_reduce<LPU, true>(e);
+  for (int i = 0; i < 4; ++i) mx = max(mx, max((int)(w[i] & 0x7FFFu), (int)((w[i] >> 16) & 0x7FFFu)));
+  mx = dpp_group_reduce<LPU, true>(mx);
+  const int e = mx >> 7;
+  int xi[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const uint32_t b16 = (w[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
-    const int xi = (int)ldexpf(bf2f(b16), 148 - e);  // exact; truncation toward zero
-    t0[i] = (uint32_t)xi;                            // limb 0 = byte 0
-    t1[i] = (uint32_t)xi + 0x80u;                    // limb 1 = byte 1
-    t2[i] = (uint32_t)xi + 0x8080u;                  // limb 2 = byte 2
+    xi[i] = (int)ldexpf(bf2f(b16), 148 - e);  // exact; truncation toward zero
   }
-  return e;
+  clamp_nonfinite(e, xi);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    t0[i] = (uint32_t)xi[i];          // limb 0 = byte 0
+    t1[i] = (uint32_t)xi[i] + 0x80u;    // limb 1 = byte 1
+    t2[i] = (uint32_t)xi[i] + 0x8080u;  // limb 2 = byte 2
+  }
+  return mx;
 }
 
 // Writes the limb bytes of inputs o0 .. o0+7 of a lane chunk: dst points at (chunk, half 0, limb 0) of the LDS operand
@@ -225,7 +249,8 @@ __device__ __forceinline__ void store_limbs(uint8_t* dst, size_t half_stride, in
 //     cleared patterns; NaN / Inf patterns order above every finite one, as their exponent fields do);
 //   - W4: the limb dwords are gathered with byte permutes and their sums taken from the same dwords (sdot4);
 //   - the limb-0 and limb-1 sums of the group share one packed reduction (|sum| <= 128 * 128 < 2^15).
-// Returns e; d0..d2 = the group's limb sums (every lane of the unit).  store = false: nothing is written.
+// Returns the group's largest magnitude pattern (act_scale_bits' argument); d0..d2 = the group's limb sums (every lane
+// of the unit).  store = false: nothing is written.
 template <int BITS>
 __device__ __forceinline__ int convert_unit(const uint4 v, uint8_t* dst, size_t half_stride, int o0, bool store,
                                             int& d0, int& d1, int& d2) {
@@ -236,16 +261,21 @@ __device__ __forceinline__ int convert_unit(const uint4 v, uint8_t* dst, size_t 
   };
   const u16x2 mx = __builtin_elementwise_max(__builtin_elementwise_max(mag(v.x), mag(v.y)),
                                              __builtin_elementwise_max(mag(v.z), mag(v.w)));
-  const int e = dpp_group_reduce<16, true>(max((int)mx.x, (int)mx.y)) >> 7;
+  const int mxg = dpp_group_reduce<16, true>(max((int)mx.x, (int)mx.y)), e = mxg >> 7;
   const uint32_t w[4] = {v.x, v.y, v.z, v.w};
   uint32_t t0[8], t1[8], t2[8];
+  int xi[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const uint32_t b16 = (w[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
-    const int xi = (int)ldexpf(bf2f(b16), 148 - e);  // exact; truncation toward zero
-    t0[i] = (uint32_t)xi;
-    t1[i] = (uint32_t)xi + 0x80u;
-    t2[i] = (uint32_t)xi + 0x8080u;
+    xi[i] = (int)ldexpf(bf2f(b16), 148 - e);  // exact; truncation toward zero
+  }
+  clamp_nonfinite(e, xi);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    t0[i] = (uint32_t)xi[i];
+    t1[i] = (uint32_t)xi[i] + 0x80u;
+    t2[i] = (uint32_t)xi[i] + 0x8080u;
   }
   int s0 = 0, s1 = 0, s2 = 0;
   if constexpr (BITS == 4) {
@@ -276,7 +306,7 @@ __device__ __forceinline__ int convert_unit(const uint4 v, uint8_t* dst, size_t 
   d2 = dpp_group_reduce<16, false>(s2);
   d0 = (int)(short)(p01 & 0xFFFF);
   d1 = (p01 - d0) >> 16;
-  return e;
+  return mxg;
 }
 
 }  // namespace

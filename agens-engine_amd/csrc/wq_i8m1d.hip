@@ -41,15 +41,6 @@
 #include "wq_common.h"
 #include "wq_i8_common.h"
 
-// phase timestamps for profiling builds (a build that defines them records them; product builds compile nothing)
-#ifndef AK_M1_STAMP
-#define AK_M1_STAMP(i)
-#define AK_M1_STAMP_AFTER(i, v)
-#define AK_M1_STAMP_ITEM(i)
-#define AK_M1_WG_BEGIN()
-#define AK_M1_WG_END()
-#endif
-
 // tile items in flight per wave (register buffers) for one or two tokens
 #ifndef AK_M1_TILES
 #define AK_M1_TILES 2
@@ -129,29 +120,6 @@ constexpr long long kChainSpinTicks = 20000000;  // 0.2 s of the 100 MHz wall cl
 __device__ __attribute__((aligned(256))) uint32_t g_chain_flags[kChainMaxWg * kChainFlagStride];
 __device__ uint32_t g_chain_err;
 
-// per-step phase timestamps of a chained launch, in probe builds only (-DAK_CHAIN_PROBE; product builds compile
-// nothing): [step][workgroup][phase] = wall clock (100 MHz) when thread 0 passed: 0 step start, 1 activations
-// requested after the wait, 2 activations converted, 3 item loop done (all waves), 4 step signalled
-#ifdef AK_CHAIN_PROBE
-constexpr int kProbeSteps = 320;
-__device__ unsigned long long g_probe[kProbeSteps * kChainMaxWg * 8];
-#define AK_PROBE(s, i)                                                                  \
-  do {                                                                                   \
-    if (threadIdx.x == 0 && (s) < kProbeSteps)                                           \
-      g_probe[((size_t)(s) * kChainMaxWg + blockIdx.x) * 8 + (i)] = wall_clock64();      \
-  } while (0)
-// per wave (lane 0): 0 item loop entered, 1 first group of items computed, 2 item loop left
-__device__ unsigned long long g_probe_w[kProbeSteps * 256 * 16 * 4];
-#define AK_PROBE_W(s, i)                                                                                 \
-  do {                                                                                                    \
-    if ((threadIdx.x & 63) == 0 && (s) < kProbeSteps && blockIdx.x < 256)                                 \
-      g_probe_w[(((size_t)(s) * 256 + blockIdx.x) * 16 + (threadIdx.x >> 6)) * 4 + (i)] = wall_clock64(); \
-  } while (0)
-#else
-#define AK_PROBE(s, i)
-#define AK_PROBE_W(s, i)
-#endif
-
 // Wave 0 polls until the flags of workgroups [0, nwg) are all at least `target` (wrap-safe).  It polls before it
 // requests weights of its own, so that no poll waits behind them.
 __device__ __forceinline__ void chain_poll(uint32_t target) {
@@ -198,9 +166,8 @@ __device__ __forceinline__ void lds_barrier() {
 // only that stripe's activations; it writes its stripe partials with device-coherent stores, and the last of the
 // range's P workgroups (device-scope counter) adds them in stripe order and writes y.
 template <int BITS, int SPLIT, int DEPTH, int MT, bool CHAIN, bool SK = false, bool ACT = false>
-__device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wait, uint32_t target, int ps = 0) {
+__device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wait, uint32_t target) {
   static_assert(!SK || SPLIT == 1, "a split launch gives every wave whole stripes of its blocks");
-  AK_PROBE(ps, 0);
   constexpr int LPU = kG / 8, UPW = 64 / LPU, XB = 4;
   constexpr int REC = 128 * BITS;  // one row's tile record
   const int P = a.P, nquad = a.nquad, k = a.k, mm = a.m;  // mm <= MT tokens (the others are zero, not written)
@@ -296,13 +263,11 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
   };
   // a chained step that depends on earlier steps requests its first weights before it waits for them (below)
   const bool late_x = CHAIN && wait;
-  AK_M1_STAMP(0);
   if (!late_x) {
     xload(0);
 #pragma unroll
     for (int b = 0; b < XB; ++b) asm volatile("" ::"v"(xv[b].x), "v"(xv[b].y), "v"(xv[b].z), "v"(xv[b].w));
   }
-  AK_M1_STAMP(1);
 
   // ---- this wave's tasks: stripe set j, tiles [ta, tb), blocks b0w, b0w + bstep, ... < nb
   const int j = wave % SPLIT, bstep = nwv / SPLIT, b0w = wave / SPLIT;
@@ -375,7 +340,6 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
     lds_barrier();
     xload(0);
   }
-  AK_PROBE(ps, 1);
 
   auto convert = [&](int p0) {
 #pragma unroll
@@ -403,8 +367,6 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
     convert(p0);
   }
   __syncthreads();
-  AK_M1_STAMP(2);
-  AK_PROBE(ps, 2);
 
   // A role: group c >> 2, limb c & 3 (limb 3 reads zeros), chunk 4 * (c >> 2) + h of the quad; half 1 is kCPQ * 48
   // bytes further
@@ -516,7 +478,6 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
   };
 
   const int nfull = nitems / DEPTH * DEPTH;
-  AK_PROBE_W(ps, 0);
   for (int i0 = 0; i0 < nfull; i0 += DEPTH) {
     float sv[DEPTH][MT];
     bool end[DEPTH];
@@ -529,7 +490,6 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d)
       if (end[d]) stripe_end(sv[d], eg[d], ep[d]);
-    if (i0 == 0) AK_PROBE_W(ps, 1);
   }
   // the last, partial group (its later fetches load the cache-resident dummy item)
 #pragma unroll
@@ -542,10 +502,7 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
       if (e) stripe_end(v, g, p);
     }
   }
-  AK_M1_STAMP(3);
-  AK_PROBE_W(ps, 2);
   __syncthreads();
-  AK_PROBE(ps, 3);
   if constexpr (SK) {
     // every wave's partial stores are acknowledged at device scope before the range's counter moves
     __builtin_amdgcn_s_waitcnt(kVmcnt0);
@@ -579,9 +536,7 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
 template <int BITS, int SPLIT, int DEPTH, int MT, bool SK = false, bool ACT = false>
 __global__ void __launch_bounds__(1024, 1) i8_m1d_kernel(const I8Args a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  AK_M1_WG_BEGIN();
   m1d_body<BITS, SPLIT, DEPTH, MT, false, SK, ACT>(a, lds, false, 0u);
-  AK_M1_WG_END();
 }
 
 size_t m1d_x_bytes(int nquad, int mt) { return 512 + (size_t)mt * nquad * (kCPQ * 96 + 4 * 16); }
@@ -738,31 +693,30 @@ __global__ void __launch_bounds__(1024, 1) i8_chain_kernel(const ChainStep* __re
     const bool w = st.wait != 0;
     const uint32_t target = f0 + (uint32_t)s;
     switch (st.kind) {
-      case 4 * 16 + 1: m1d_body<4, 1, D, MT, true>(st.a, lds, w, target, s); break;
-      case 4 * 16 + 2: m1d_body<4, 2, D, MT, true>(st.a, lds, w, target, s); break;
-      case 4 * 16 + 4: m1d_body<4, 4, D, MT, true>(st.a, lds, w, target, s); break;
-      case 4 * 16 + 8: m1d_body<4, 8, D, MT, true>(st.a, lds, w, target, s); break;
-      case 3 * 16 + 1: m1d_body<3, 1, D, MT, true>(st.a, lds, w, target, s); break;
-      case 3 * 16 + 2: m1d_body<3, 2, D, MT, true>(st.a, lds, w, target, s); break;
-      case 3 * 16 + 4: m1d_body<3, 4, D, MT, true>(st.a, lds, w, target, s); break;
-      case 3 * 16 + 8: m1d_body<3, 8, D, MT, true>(st.a, lds, w, target, s); break;
-      case 2 * 16 + 1: m1d_body<2, 1, D, MT, true>(st.a, lds, w, target, s); break;
-      case 2 * 16 + 2: m1d_body<2, 2, D, MT, true>(st.a, lds, w, target, s); break;
-      case 2 * 16 + 4: m1d_body<2, 4, D, MT, true>(st.a, lds, w, target, s); break;
-      case kSplitK + 4 * 16 + 1: m1d_body<4, 1, D, MT, true, true>(st.a, lds, w, target, s); break;
-      case kSplitK + 3 * 16 + 1: m1d_body<3, 1, D, MT, true, true>(st.a, lds, w, target, s); break;
-      case kSplitK + 2 * 16 + 1: m1d_body<2, 1, D, MT, true, true>(st.a, lds, w, target, s); break;
-      case kAct + kSplitK + 4 * 16 + 1: m1d_body<4, 1, D, MT, true, true, true>(st.a, lds, w, target, s); break;
-      case kAct + kSplitK + 3 * 16 + 1: m1d_body<3, 1, D, MT, true, true, true>(st.a, lds, w, target, s); break;
-      case kAct + kSplitK + 2 * 16 + 1: m1d_body<2, 1, D, MT, true, true, true>(st.a, lds, w, target, s); break;
-      default: m1d_body<2, 8, D, MT, true>(st.a, lds, w, target, s); break;
+      case 4 * 16 + 1: m1d_body<4, 1, D, MT, true>(st.a, lds, w, target); break;
+      case 4 * 16 + 2: m1d_body<4, 2, D, MT, true>(st.a, lds, w, target); break;
+      case 4 * 16 + 4: m1d_body<4, 4, D, MT, true>(st.a, lds, w, target); break;
+      case 4 * 16 + 8: m1d_body<4, 8, D, MT, true>(st.a, lds, w, target); break;
+      case 3 * 16 + 1: m1d_body<3, 1, D, MT, true>(st.a, lds, w, target); break;
+      case 3 * 16 + 2: m1d_body<3, 2, D, MT, true>(st.a, lds, w, target); break;
+      case 3 * 16 + 4: m1d_body<3, 4, D, MT, true>(st.a, lds, w, target); break;
+      case 3 * 16 + 8: m1d_body<3, 8, D, MT, true>(st.a, lds, w, target); break;
+      case 2 * 16 + 1: m1d_body<2, 1, D, MT, true>(st.a, lds, w, target); break;
+      case 2 * 16 + 2: m1d_body<2, 2, D, MT, true>(st.a, lds, w, target); break;
+      case 2 * 16 + 4: m1d_body<2, 4, D, MT, true>(st.a, lds, w, target); break;
+      case kSplitK + 4 * 16 + 1: m1d_body<4, 1, D, MT, true, true>(st.a, lds, w, target); break;
+      case kSplitK + 3 * 16 + 1: m1d_body<3, 1, D, MT, true, true>(st.a, lds, w, target); break;
+      case kSplitK + 2 * 16 + 1: m1d_body<2, 1, D, MT, true, true>(st.a, lds, w, target); break;
+      case kAct + kSplitK + 4 * 16 + 1: m1d_body<4, 1, D, MT, true, true, true>(st.a, lds, w, target); break;
+      case kAct + kSplitK + 3 * 16 + 1: m1d_body<3, 1, D, MT, true, true, true>(st.a, lds, w, target); break;
+      case kAct + kSplitK + 2 * 16 + 1: m1d_body<2, 1, D, MT, true, true, true>(st.a, lds, w, target); break;
+      default: m1d_body<2, 8, D, MT, true>(st.a, lds, w, target); break;
     }
     // signal: this workgroup's outputs of steps <= s are stored (each wave waits for its own stores' acknowledgement,
     // which for sc1 stores means written through to device scope)
     __builtin_amdgcn_s_waitcnt(kVmcnt0);
     __syncthreads();
     if (threadIdx.x == 0) __hip_atomic_store(flag, f0 + (uint32_t)s + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    AK_PROBE(s, 4);
   }
 }
 
@@ -884,15 +838,6 @@ int m1d_chain_launch(const void* table, int nsteps, int mt, size_t smem, hipStre
     hipLaunchKernelGGL(i8_chain_kernel<2>, dim3(num_cus()), dim3(1024), smem, s, t, nsteps);
   return (int)hipGetLastError();
 }
-
-#ifdef AK_CHAIN_PROBE
-extern "C" int ak_chain_probe_read(void* dst, size_t bytes) {
-  return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_probe), bytes, 0, hipMemcpyDeviceToHost);
-}
-extern "C" int ak_chain_probe_read_w(void* dst, size_t bytes) {
-  return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_probe_w), bytes, 0, hipMemcpyDeviceToHost);
-}
-#endif
 
 // reads and clears the flag a chained launch raises when a wait ran out (0.2 s): 1 if one did since the last call
 int m1d_chain_error(int* err) {

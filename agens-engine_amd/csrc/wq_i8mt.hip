@@ -30,11 +30,6 @@
 #include "wq_common.h"
 #include "wq_i8_common.h"
 
-// phase timestamps for profiling builds (a build that defines them records them; product builds compile nothing)
-#ifndef AK_M1_STAMP
-#define AK_M1_STAMP(i)
-#endif
-
 namespace agq {
 
 int num_cus();
@@ -208,11 +203,9 @@ __global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
       }
     }
   };
-  AK_M1_STAMP(0);
   xload(0);
 #pragma unroll
   for (int b = 0; b < XB; ++b) asm volatile("" ::"v"(xv[b].x), "v"(xv[b].y), "v"(xv[b].z), "v"(xv[b].w));
-  AK_M1_STAMP(1);
 
   // ---- this wave's tasks: stripe set j, quads [qa, qb), blocks b0w, b0w + bstep, ... < nb
   const int j = wave % SPLIT, bstep = nwv / SPLIT, b0w = wave / SPLIT;
@@ -300,14 +293,11 @@ __global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
     }
   };
   convert(0);
-  AK_M1_STAMP(5);
   for (int p0 = XB; p0 < npass; p0 += XB) {
     xload(p0);
     convert(p0);
   }
-  AK_M1_STAMP(6);
   __syncthreads();
-  AK_M1_STAMP(2);
 
   // A role: token (c >> 2) of the token group, limb c & 3 (limb 3 reads zeros at the pass's 4 free bank slots)
   const bool a_on = (c & 3) < 3;
@@ -444,7 +434,6 @@ __global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
   } else {
     run_chunk(0);
   }
-  AK_M1_STAMP(3);
   if constexpr (SK) {
     // every wave's partial stores are acknowledged at device scope before the range's counter moves
     __builtin_amdgcn_s_waitcnt(kVmcnt0);
@@ -456,7 +445,6 @@ __global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
       if (old == P - 1) __hip_atomic_store(scnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next launch
     }
     __syncthreads();
-    AK_M1_STAMP(4);
     if (!*last) return;
     __syncthreads();  // every thread has read the flag before the outputs overwrite it
     for (int i = tid; i < nb * MP * 16; i += 64 * nwv) {
@@ -566,11 +554,14 @@ int launch_mt(I8Args a, hipStream_t s) {
     }
     // 9..16 tokens, one segment, one stripe's 16-token image beyond the LDS: both 8-token halves in one split-K
     // launch (NT = 2 each, the same results as two 8-token launches).  Half the row ranges per half keep the grid at
-    // one workgroup per CU, and the two halves of a (range, stripe) run at once on the same XCD (workgroups 128 apart),
+    // one workgroup per CU, and the two halves of a (range, stripe) run at once on the same XCD (workgroups nrh * P apart),
     // so the second one's weights come from the L2: down 5120 x 27648 at 16 tokens, W2 / W3 / W4 44.8 / 59.6 / 54.4 ->
     // 30.4 / 42.9 / 40.7 us (full ranges per half, two rounds of workgroups: 43.3 / 57.1 / 52.5 us).
     if constexpr (NT == 4) {
-      const int nrh = nrt / 2 > 0 ? nrt / 2 : 1;  // row ranges per half
+      // row ranges per half, a multiple of 8 / gcd(P, 8) so that nrh * P is a multiple of the 8 XCDs (workgroup i runs
+      // on XCD i % 8: the two halves of a (range, stripe), nrh * P workgroups apart, then share an XCD's L2)
+      const int xq = 8 / (a.P % 8 == 0 ? 8 : a.P % 4 == 0 ? 4 : a.P % 2 == 0 ? 2 : 1);
+      const int nrh = nrt / 2 / xq * xq > 0 ? nrt / 2 / xq * xq : xq;
       const int nbs = (g.n[0] + 15) / 16, nbr2 = (nbs + nrh - 1) / nrh;
       const size_t smem2 = 256 + (size_t)mt_a_bytes(cg, 2) + mt_meta_bytes(cg, 2) + (size_t)nbr2 * 4 * 2 * 16 * 2 + 16;
       const size_t pf = (size_t)a.P * 4 * 2 * nbs * 16;  // one half's stripe partials (floats)

@@ -69,8 +69,14 @@ int ak_w4g128_repack_kt(const int32_t* packed, const void* scales, void* wt, voi
  * (ldy == NULL: n[i]).  1 <= m <= 128, 1 <= nseg <= 4, the segments share x, k, group and bits.
  * Numerics (both deterministic; every output row is bit-identical for any m, any segmentation and any bit width
  * holding the same values):
- *   default  -- integer MFMA: exact per-group integer dot products of q with x, rounded once to fp32, scaled and
- *               accumulated in fp32 in a fixed order;
+ *   default  -- integer MFMA: per group of inputs, x as fixed point relative to the group's largest input,
+ *               x_int = trunc(x * 2^(148 - E)) with E that input's exponent field (22 bits: inputs below 2^-14 of the
+ *               group's largest lose their low bits), the integer dot product of q with x_int exact, rounded once
+ *               to fp32, scaled and accumulated in fp32 in a fixed order.  Non-finite inputs: a group holding a NaN
+ *               adds NaN; one holding an Inf (no NaN) adds S * scale * Inf, S the sum of sign(x) * q over its Infs
+ *               (+-Inf, or NaN where S = 0: the fp32 path's value wherever the group's Inf products share a sign).
+ *               Groups whose largest input is below about 2^-100 lose precision to the underflow of the fp32 scale
+ *               product (absolute errors below 2^-100);
  *   exact    -- the reference's fp32 FMA path, bit for bit (ak_w4_set_mma(0) or AGENS_W4_EXACT=1);
  *   bf16w=1  -- weights rounded to bf16(q * scale) first (Marlin numerics), always on the fp32 path. */
 int ak_wq_gemv_kt_multi(int bits, const void* x, int m, int nseg, const void* const* wt, const void* const* st,

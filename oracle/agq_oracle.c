@@ -309,7 +309,11 @@ static void group_limb_sums(const uint16_t* xr, const int8_t* q, int k, int g0, 
   D[0] = D[1] = D[2] = 0;
   for (int i = g0; i < g0 + group; ++i) {
     if (i >= k) continue;
-    const long long xi = (long long)ldexp((double)ora_bf2f(xr[i]), 148 - e); /* truncation toward zero */
+    long long xi;
+    if (e == 255) /* a non-finite group: an Inf counts as its sign, every other input (finite or NaN) as 0 */
+      xi = (xr[i] & 0x7FFF) == 0x7F80 ? ((xr[i] & 0x8000) ? -1 : 1) : 0;
+    else
+      xi = (long long)ldexp((double)ora_bf2f(xr[i]), 148 - e); /* truncation toward zero */
     const long long x1 = (xi + 128) >> 8, x2 = (x1 + 128) >> 8;           /* arithmetic shifts */
     const long long d0 = xi - x1 * 256, d1 = x1 - x2 * 256, d2 = x2;
     D[0] += d0 * q[i];
@@ -317,6 +321,16 @@ static void group_limb_sums(const uint16_t* xr, const int8_t* q, int k, int g0, 
     D[2] += d2 * q[i];
   }
   *E = e;
+}
+
+/* The activation scale of a group with largest exponent field E: 2^(E - 148); a group holding a NaN: NaN; one holding
+ * an Inf and no NaN: +Inf (with its Inf inputs counted as +-1 above, the group adds S * scale * Inf, S the sum of
+ * sign(x) * q over them: +-Inf, or NaN where S = 0). */
+static float act_scale(const uint16_t* xr, int k, int g0, int group, int E) {
+  if (E < 255) return ldexpf(1.0f, E - 148);
+  for (int i = g0; i < g0 + group && i < k; ++i)
+    if ((xr[i] & 0x7FFF) > 0x7F80) return NAN;
+  return INFINITY;
 }
 
 static long long group_sum(const uint16_t* xr, const int8_t* q, int k, int g0, int group, int* E) {
@@ -359,7 +373,7 @@ void ora_gemv_fast_kt_rows(int bits, const uint16_t* x, int m, const uint8_t* wt
           group_limb_sums(xr, q, k, g * group, group, &E, D);
           const int T = (int)(D[2] * 256 + D[1]);
           const float gsum = fmaf((float)T, 256.0f, (float)D[0]);
-          const float sE = ora_bf2f(st[((size_t)t * n + o) * SPT + gi]) * ldexpf(1.0f, E - 148);
+          const float sE = ora_bf2f(st[((size_t)t * n + o) * SPT + gi]) * act_scale(xr, k, g * group, group, E);
           acc[p][s] = fmaf(gsum, sE, acc[p][s]);
         }
       }

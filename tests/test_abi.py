@@ -64,6 +64,7 @@ def test_invalid_arguments_return_1_without_a_gpu(K):
     assert K.ak_bf16_gemv_bi(one, one, None, one, 0, 16, 1024, None) == 1
     assert K.ak_bf16_gemv_bi(one, one, None, one, 129, 16, 1024, None) == 1
     assert K.ak_bf16_gemv_bi_ld(one, one, None, one, 1, 16, 1040, 16, None) == 1
+    assert K.ak_bf16_gemv_bi_ld(one, one, None, one, 2, 16, 1024, 15, None) == 1  # ldy < n: token rows overlap
     # silu_mul.cu:59 / :67: sizes not multiples of 8, a share past the row -> 1
     assert K.ak_silu_mul(one, one, 2, 100, None) == 1
     assert K.ak_silu_mul_part(one, one, 64, 4, 8, None) == 1

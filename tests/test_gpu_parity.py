@@ -370,6 +370,13 @@ def test_long_k_nine_to_sixteen_tokens(bits, m):
     lo = y_of(gemv(bits, X, 8, [A], k, g)[0], 8, n)
     hi = y_of(gemv(bits, X.addr(8 * k * 2), m - 8, [A], k, g)[0], m - 8, n)
     assert np.array_equal(y1[:8], lo) and np.array_equal(y1[8:], hi)
+    # a strided output (ldy > n): the same rows, the padding columns untouched (token rows 8.. of the second half)
+    ld = n + 24
+    Ys = Dev.of(np.full(m * ld, 0x7FC1, dtype=np.uint16))
+    gemv(bits, X, m, [A], k, g, ldy=[ld], ys=[Ys])
+    ys = Ys.get(np.uint16, m * ld).reshape(m, ld)
+    assert np.array_equal(ys[:, :n], y1)
+    assert (ys[:, n:] == 0x7FC1).all()
     wt, st = A.host_kt()
     for r0 in (0, 448, n - 40):
         yo = ora_fast(bits, x, m, wt, st, n, k, g, rows=(r0, r0 + 40))

@@ -342,3 +342,40 @@ def test_exact_order_known_answers(case, bf16w):
     x, wt, st = exact_order_case(vals)
     y = ora_exact(4, x, 1, wt, st, 1, 4096, 128, bf16w=bf16w)
     assert bf2f_array(y.reshape(-1))[0] == want
+
+
+@pytest.mark.parametrize("bits", [4, 3, 2])
+def test_fast_nonfinite_activations_like_fp32_path(bits):
+    # The default numerics' definition for non-finite activations, pinned against the reference's fp32 path
+    # (reference.rs:53-71, restated by ora_gemv_ref_f32): with one Inf per group every output is NaN / +Inf / -Inf
+    # exactly where the fp32 path's is (an Inf times q = 0 is NaN there, S = 0 here; Infs of two groups with opposite
+    # signs meet as Inf - Inf); a NaN input makes every output NaN; a token without non-finite inputs is unaffected.
+    n, k, group = 64, 2048, 128
+    lo, span = -(1 << (bits - 1)), 1 << bits
+    packed = gen_container(61 + bits, n, k, lo, span)
+    scales = gen_scales(62, n * k // group)
+    rc, wt, st = ora_repack(bits, packed, scales, n, k, group)
+    assert rc == 0
+    m = 4
+    x = gen_x(63, m * k).reshape(m, k)
+    clean = x[3].copy()
+    x[0, 130] = 0x7F80                      # +Inf in group 1
+    x[1, 5], x[1, 2000] = 0xFF80, 0x7F80    # -Inf in group 0, +Inf in group 15
+    x[2, 300] = 0x7FC0                      # NaN in group 2
+    x = x.reshape(-1)
+    y = bf2f_array(ora_fast(bits, x, m, wt, st, n, k, group))
+    ref = ora_ref_f32(x, m, packed, scales, n, k, group)
+    for t in (0, 1):
+        assert np.array_equal(np.isnan(y[t]), np.isnan(ref[t]))
+        assert np.array_equal(np.isposinf(y[t]), np.isposinf(ref[t]))
+        assert np.array_equal(np.isneginf(y[t]), np.isneginf(ref[t]))
+    # rows whose weight at the Inf input is 0 are NaN in both; the others +-Inf with the sign of q
+    q = np.zeros(n * k, dtype=np.int8)
+    for o in range(n):
+        oracle().ora_unpack_row(ptr(packed[o * k // 8:]), k, ptr(q[o * k:]))
+    q = q.reshape(n, k)
+    assert np.array_equal(np.isnan(y[0]), q[:, 130] == 0)
+    assert np.array_equal(np.isposinf(y[0]), q[:, 130] > 0)
+    assert np.all(np.isnan(y[2]))
+    one = bf2f_array(ora_fast(bits, clean, 1, wt, st, n, k, group))[0]
+    assert np.array_equal(one, y[3])
