@@ -1,12 +1,14 @@
-// GEMV entry points of the C ABI: argument rules, routing between the two numerics and token chunking.  The kernels
-// use no scratch memory: every launch is self-contained (stripe partials meet in LDS), so the entry points allocate
-// nothing and are safe under stream capture.
+// GEMV entry points of the C ABI: argument rules, routing between the two numerics and token chunking.  Split-K
+// launches keep stripe partials and row-range counters in library scratch (per (device, stream), allocated on first
+// use outside a stream capture; under a capture without it a route without scratch is taken), or, for
+// ak_wq_gemv_kt_multi_noalloc, in a static device array; every other launch is self-contained (partials meet in LDS).
 //
 // Argument rules and return codes follow the reference (kernels/src/w4_gemv.cu:702-731, :852-876, :898-935,
 // :3265-3282): group in {64, 128} with k % group == 0, 1 <= nseg <= 4, 1 <= m <= 128; error 1 otherwise.
 #include <stdlib.h>
 #include <string.h>
 
+#include <mutex>
 #include <new>
 
 #include "agens_kernels.h"
@@ -136,6 +138,51 @@ int run_step(const ak_wq_step& st, hipStream_t s) {
   return gemv(st.bits, st.x, st.m, st.nseg, st.wt, st.st, st.y, st.n, ldy, st.k, st.group, st.bf16w, false, s, st.act);
 }
 
+// ---- the entry point that allocates nothing: split-K partials and counters in a static device array
+//
+// Bytes of split-K scratch any route of one launch of at most 16 tokens can ask for: 4 KB of row-range counters,
+// then P (<= 8) stripe partials per token (padded to T = 4, 8 or 16: the kernels' token groups) per output row (padded
+// to 16-row blocks), 4 bytes each; chunks of 16 tokens reuse it in stream order.
+constexpr size_t kNoAllocScratchBytes = (size_t)64 << 20;
+__device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+size_t noalloc_scratch_need(int m, int nseg, const int* n, int k) {
+  const int tiles = kpad(k) / 1024, P = tiles < 8 ? tiles : 8;
+  const int mm = m < 16 ? m : 16, T = mm <= 4 ? 4 : mm <= 8 ? 8 : 16;
+  size_t blocks = 0;
+  for (int i = 0; i < nseg; ++i) blocks += (size_t)(n[i] + 15) / 16;
+  return 4096 + (size_t)P * T * blocks * 16 * 4;
+}
+
+__global__ void zero_words_kernel(uint32_t* p, int nwords) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < nwords; i += gridDim.x * blockDim.x) p[i] = 0u;
+}
+
+// The device address of `scratch` on the current device (hipGetSymbolAddress once per device, with that device
+// current), and at that first call its counter words cleared by a fill kernel on `s` (the kernels return every counter
+// to zero at the end of each launch).  In host code `scratch` itself is only a stand-in: kernels get this address.
+int noalloc_scratch(hipStream_t s, void** out) {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static void* addr[kMaxDevices] = {};
+  int dev = 0;
+  int e = (int)hipGetDevice(&dev);
+  if (e) return e;
+  if (dev < 0 || dev >= kMaxDevices) return AK_INVALID;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!addr[dev]) {
+    void* p = nullptr;
+    e = (int)hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e) return e;
+    hipLaunchKernelGGL(zero_words_kernel, dim3(4), dim3(256), 0, s, static_cast<uint32_t*>(p), 4096 / 4);
+    e = (int)hipGetLastError();
+    if (e) return e;
+    addr[dev] = p;
+  }
+  *out = addr[dev];
+  return 0;
+}
+
 }  // namespace
 }  // namespace agq
 
@@ -146,6 +193,28 @@ extern "C" {
 int ak_wq_gemv_kt_multi(int bits, const void* x, int m, int nseg, const void* const* wt, const void* const* st,
                         void* const* y, const int* n, const int* ldy, int k, int group, int bf16w, void* stream) {
   return gemv(bits, x, m, nseg, wt, st, y, n, ldy, k, group, bf16w, false, static_cast<hipStream_t>(stream));
+}
+
+// ak_wq_gemv_kt_multi that allocates nothing (no counterpart in the reference; for callers that cannot allocate:
+// code under stream capture, tight serving loops): its split-K launches use the library's static 64 MiB device
+// array instead of per-stream scratch.  1 (invalid value) when the call's worst-case split-K scratch
+// (noalloc_scratch_need) exceeds it, e.g. a 152064-row linear at 16 tokens.  Calls on one device share the array:
+// calls that overlap in time on one device race.
+int ak_wq_gemv_kt_multi_noalloc(int bits, const void* x, int m, int nseg, const void* const* wt, const void* const* st,
+                                void* const* y, const int* n, const int* ldy, int k, int group, int bf16w,
+                                void* stream) {
+  if (nseg < 1 || nseg > kMaxSegs || !n || m < 1 || k < 1) return AK_INVALID;
+  for (int i = 0; i < nseg; ++i)
+    if (n[i] < 1) return AK_INVALID;
+  if (noalloc_scratch_need(m, nseg, n, k) > kNoAllocScratchBytes) return AK_INVALID;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  void* p = nullptr;
+  if (const int e = noalloc_scratch(s, &p)) return e;
+  ScratchOverride& o = scratch_override();
+  o = {p, kNoAllocScratchBytes, true};
+  const int e = gemv(bits, x, m, nseg, wt, st, y, n, ldy, k, group, bf16w, false, s);
+  o = ScratchOverride();
+  return e;
 }
 
 int ak_wq_gemv_kt_silu(int bits, const void* gate_up, int m, const void* wt, const void* st, void* y, int n, int ldy,

@@ -31,6 +31,15 @@ struct Segs {
 
 __host__ __device__ inline int kpad(int k) { return (k + 1023) & ~1023; }
 
+// A fixed scratch buffer that replaces the per-stream library scratch for the calling host thread while `on` (the
+// entry point that allocates nothing installs it around its launches).
+struct ScratchOverride {
+  void* p = nullptr;
+  size_t bytes = 0;
+  bool on = false;
+};
+ScratchOverride& scratch_override();
+
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 

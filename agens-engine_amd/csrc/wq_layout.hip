@@ -28,7 +28,17 @@ int num_cus() {
 // capture (null then: the caller takes a path without scratch), held until the process ends.  Launches on one stream
 // are ordered, so they share it safely; before a buffer is replaced the stream is synchronized (earlier launches may
 // still use it).  Users keep their counters at zero between launches.
+//
+// A caller that must not allocate (ak_wq_gemv_kt_multi_noalloc) installs a fixed buffer for the calling thread first:
+// then this returns that buffer when it is large enough and null otherwise, and never allocates.
+ScratchOverride& scratch_override() {
+  static thread_local ScratchOverride o;
+  return o;
+}
+
 void* stream_scratch(hipStream_t s, size_t bytes) {
+  const ScratchOverride& o = scratch_override();
+  if (o.on) return bytes <= o.bytes ? o.p : nullptr;
   static std::mutex mu;
   static std::map<std::pair<int, hipStream_t>, std::pair<void*, size_t>> bufs;
   int dev = 0;

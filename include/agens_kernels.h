@@ -82,6 +82,16 @@ int ak_w4g128_repack_kt(const int32_t* packed, const void* scales, void* wt, voi
 int ak_wq_gemv_kt_multi(int bits, const void* x, int m, int nseg, const void* const* wt, const void* const* st,
                         void* const* y, const int* n, const int* ldy, int k, int group, int bf16w,
                         void* stream);            /* agens_kernels.h:258-259, w4_gemv.cu:852-876 */
+/* No counterpart in the reference: ak_wq_gemv_kt_multi that allocates nothing, for callers that cannot call hipMalloc
+ * (code under stream capture, tight serving loops, harnesses that forbid allocation).  Same arguments, results and
+ * error codes; its split-K launches keep their partials and counters in a static 64 MiB device array of the library
+ * (one per GPU, held until the process ends) instead of per-stream scratch.  Returns 1 when the call's worst-case
+ * scratch, 4096 + 64 * P * T * sum_i ceil(n[i] / 16) bytes (P = min(8, ceil(k / 1024)), T = 4, 8 or 16 for up to 4,
+ * 8 or more tokens), exceeds it (e.g. a 152064-row linear at more than 8 tokens).  Calls that overlap in time on one
+ * GPU share the array and race: keep them on one stream. */
+int ak_wq_gemv_kt_multi_noalloc(int bits, const void* x, int m, int nseg, const void* const* wt,
+                                const void* const* st, void* const* y, const int* n, const int* ldy, int k, int group,
+                                int bf16w, void* stream);
 int ak_w4_gemv_kt(const void* x, const void* wt, const void* st, void* y, int n, int k, int group, int bf16w,
                   void* stream);                  /* agens_kernels.h:195-196, w4_gemv.cu:702-710 */
 int ak_w4_gemv_kt_multi(const void* x, int nseg, const void* const* wt, const void* const* st, void* const* y,

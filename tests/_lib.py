@@ -279,6 +279,7 @@ def kernels():
             "ak_wq_repack_kt": (i, [i, vp, vp, vp, vp, i, i, i, vp]),
             "ak_w4g128_repack_kt": (i, [vp, vp, vp, vp, i, i, vp]),
             "ak_wq_gemv_kt_multi": (i, [i, vp, i, i, vp, vp, vp, vp, vp, i, i, i, vp]),
+            "ak_wq_gemv_kt_multi_noalloc": (i, [i, vp, i, i, vp, vp, vp, vp, vp, i, i, i, vp]),
             "ak_w4_gemv_kt": (i, [vp, vp, vp, vp, i, i, i, i, vp]),
             "ak_w4_gemv_kt_multi": (i, [vp, i, vp, vp, vp, vp, i, i, i, vp]),
             "ak_w4_gemv_kt_batched": (i, [vp, vp, vp, vp, i, i, i, i, i, vp]),

@@ -65,6 +65,10 @@ def test_invalid_arguments_return_1_without_a_gpu(K):
     assert K.ak_bf16_gemv_bi(one, one, None, one, 129, 16, 1024, None) == 1
     assert K.ak_bf16_gemv_bi_ld(one, one, None, one, 1, 16, 1040, 16, None) == 1
     assert K.ak_bf16_gemv_bi_ld(one, one, None, one, 2, 16, 1024, 15, None) == 1  # ldy < n: token rows overlap
+    # the no-alloc GEMV refuses a call whose worst-case split-K scratch, 4096 + 64 * P * T * sum(ceil(n / 16)) bytes,
+    # exceeds its 64 MiB static array (here 8 * 16 * 8750 blocks), before any device call
+    ns = (ctypes.c_int * 1)(140000)
+    assert K.ak_wq_gemv_kt_multi_noalloc(4, one, 16, 1, None, None, None, ns, None, 8192, 128, 0, None) == 1
     # silu_mul.cu:59 / :67: sizes not multiples of 8, a share past the row -> 1
     assert K.ak_silu_mul(one, one, 2, 100, None) == 1
     assert K.ak_silu_mul_part(one, one, 64, 4, 8, None) == 1
