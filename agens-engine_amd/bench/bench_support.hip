@@ -430,6 +430,7 @@ int agb_time_xover(int bits, const void* x, int m, const void* const* wts, const
       void* yy = y;
       return ak_wq_gemv_kt_multi(bits, x, m, 1, &w, &sc, &yy, &n, nullptr, k, 128, 0, s);
     }
+    if (mode == 2) return ak_wq_gemm_kt(bits, x, m, w, sc, y, n, 0, k, 128, s);  // the fused prefill GEMM
     int r = ak_wq_dequant_kt_rows(bits, w, sc, wdense, n, k, 128, 0, n, s);
     if (!r) r = ak_bf16_linear_f32reduce(x, wdense, y, m, n, k, s);
     return r;

@@ -112,8 +112,36 @@ int tile_rows(int k, int n) {
 
 void set_prefill_tile_bytes(size_t bytes) { g_tile_bytes = bytes; }
 
+namespace {
+int g_prefill_route = -1;  // -1: by shape, 0: dequantized tiles x library GEMM, 1: the fused GEMM
+
+// The fused prefill GEMM (ak_wq_gemm_kt) against dequantized tiles x rocBLAS, measured on MI355X (us per call):
+//   gate_up W3 55296 x 5120:  m = 256: 273 vs 381, m = 512: 500 vs 475;
+//   down W2 5120 x 27648:     m = 256: 339 vs 528, m = 512: 345 vs 390;
+//   o W4 5120 x 5120:         m = 256:  71 vs  61, m = 512:  74 vs  58.
+// The fused kernel wins on long k and on wide linears up to a few hundred tokens; the library GEMM on narrow,
+// short-k linears (too few 128 x 128 tiles for the CUs) and at large m (the fused kernel expands every weight once per
+// 128 tokens).
+bool prefill_fused(int n, int k, int m) {
+  if (g_prefill_route >= 0) return g_prefill_route == 1;
+  return k >= 16384 || (n >= 16384 && m <= 384);
+}
+}  // namespace
+
+void set_prefill_route(int mode) { g_prefill_route = mode < 0 ? -1 : (mode ? 1 : 0); }
+
 int linear(const QuantLinear& t, const void* x, void* y, int m, int n, int k, int bf16w, void* stream) {
   if (t.n != n || t.k != k || m < 1 || t.np < 1 || t.np > 2) return 1;
+  if (m > 128 && prefill_fused(n, k, m)) {
+    // prefill through the fused GEMM: one launch per part, straight from the KT weights into its columns of y
+    for (int j = 0; j < t.np; ++j) {
+      const QuantPart& q = t.p[j];
+      if (const int e = ak_wq_gemm_kt(q.bits, x, m, q.wt, q.st, static_cast<uint16_t*>(y) + q.r0, q.n, n, k, q.group,
+                                      stream))
+        return e;
+    }
+    return 0;
+  }
   if (m > 128) {
     // prefill (m1_model.cu:1876-1897): dequantize a tile of output rows at a time into the bounded scratch and GEMM
     // that column tile of y (tiles by output row whatever the parts)

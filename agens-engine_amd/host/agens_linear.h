@@ -69,12 +69,18 @@ struct QuantLinear {
 };
 
 // The model's linear (m1_model.cu:1857-1900): y[m][n] = x[m][k] W^T.  Up to 128 tokens one ak_wq_gemv_kt_multi per
-// part with ldy = n; above, the prefill route: tiles of output rows dequantized (ak_wq_dequant_kt_rows) into a bounded
-// scratch of the process and multiplied by ak_bf16_linear_f32reduce(_ld).  Returns 0 or an error code; 1 for a shape
+// part with ldy = n; above, the prefill route (set_prefill_route): the fused GEMM ak_wq_gemm_kt per part, or tiles of
+// output rows dequantized (ak_wq_dequant_kt_rows) into a bounded scratch of the process and multiplied by
+// ak_bf16_linear_f32reduce(_ld).  Returns 0 or an error code; 1 for a shape
 // mismatch.  The prefill route allocates its scratch on first use (not under stream capture) and is not re-entrant.
 int linear(const QuantLinear& t, const void* x, void* y, int m, int n, int k, int bf16w, void* stream);
 // bytes of one dequantized prefill tile (default 64 MB; the reference's tile bound, m1_model.cu:1822-1826)
 void set_prefill_tile_bytes(size_t bytes);
+// The prefill route above 128 tokens: -1 by shape (the default: the fused dequantize-in-GEMM kernel ak_wq_gemm_kt on
+// long-k linears, and on wide linears up to 384 tokens, where it was measured faster), 0 dequantized tiles x library
+// GEMM (the reference's route), 1 the fused kernel.  Both give results within fp32-accumulation tolerance of the
+// dequantized weights times x.
+void set_prefill_route(int mode);
 
 // Linears sharing x (m1_model.cu:1904-1937): one launch per (bits, group) class of single-part linears when m == 1
 // (outputs bit-identical to separate GEMVs), otherwise one linear() each.

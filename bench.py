@@ -428,7 +428,7 @@ def run_xover(args, K, B):
         wd = ctx.alloc(n * k * 2)
         ctx.check(B.agb_gen_x(SEED + 41, mmax * k, 1.0, x, None), "gen x")
         row = {"config": "xover", "linear": name, "bits": bits, "n": n, "k": k, "copies": len(lins),
-               "us_gemv": {}, "us_dequant_gemm": {}}
+               "us_gemv": {}, "us_dequant_gemm": {}, "us_fused_gemm": {}}
         for m in ms_list:
             t = ctypes.c_float()
             if m <= 128:
@@ -438,6 +438,9 @@ def run_xover(args, K, B):
             ctx.check(B.agb_time_xover(bits, x, m, wts, sts, len(lins), wd, y, n, k, 1, 2, 10, ctypes.byref(t)),
                       "dequant + gemm")
             row["us_dequant_gemm"][m] = round(t.value * 1e3, 2)
+            ctx.check(B.agb_time_xover(bits, x, m, wts, sts, len(lins), wd, y, n, k, 2, 2, 10, ctypes.byref(t)),
+                      "fused gemm")
+            row["us_fused_gemm"][m] = round(t.value * 1e3, 2)
         faster = [m for m in row["us_gemv"] if row["us_dequant_gemm"][m] < row["us_gemv"][m]]
         row["crossover_m"] = min(faster) if faster else None
         lines.append(row)

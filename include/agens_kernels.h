@@ -139,6 +139,16 @@ int ak_bf16_linear_f32reduce(const void* x, const void* w, void* y, int m, int n
 int ak_bf16_linear_f32reduce_ld(const void* x, const void* w, void* y, int m, int n, int k, int ldy,
                                 void* stream);    /* agens_kernels.h:56, bf16_linear.cu:68-80 */
 
+/* ---------------------------------------------------------------------------------------------- fused prefill GEMM
+ * No single counterpart in the reference: ak_wq_dequant_kt_rows followed by ak_bf16_linear_f32reduce_ld in one kernel,
+ * the pair the model's linear() runs above 128 tokens (kernels/m1/m1_model.cu:1876-1897, w4_gemv.cu:877-895,
+ * bf16_linear.cu:68-80).  y[t][o] (row stride ldy; 0: n) = bf16(sum_i x[t][i] * w[o][i]) for every token t < m and
+ * row o < n of a KT linear, w[o][i] = bf16_rn(q * scale) (the dequantized values, bit for bit), fp32 accumulation in
+ * this kernel's order (within fp32-accumulation error of the two-call route); no scratch, no weight copy.  group in
+ * {64, 128}, k % group == 0, ldy >= n, else 1. */
+int ak_wq_gemm_kt(int bits, const void* x, int m, const void* wt, const void* st, void* y, int n, int ldy, int k,
+                  int group, void* stream);
+
 /* ---------------------------------------------------------------------------------------------- INT8 LM head GEMV
  * W8A16: y[j][o] (row stride ldy) = bf16(scale[o] * sum_i x[j][i] * q[o][i]); q int8 [n][k] row-major, scale fp32 [n]
  * (per-row symmetric), x bf16 [m][k]; 1 <= m <= 16, k % 16 == 0 (else 1).  The reference's fp32 order (32 chunk-strided

@@ -299,6 +299,7 @@ def kernels():
             "ak_bf16_linear_f32reduce": (i, [vp, vp, vp, i, i, i, vp]),
             "ak_bf16_linear_f32reduce_ld": (i, [vp, vp, vp, i, i, i, i, vp]),
             "ak_i8_gemv": (i, [vp, vp, vp, vp, i, i, i, i, vp]),
+            "ak_wq_gemm_kt": (i, [i, vp, i, vp, vp, vp, i, i, i, i, vp]),
             "ak_bf16_gemv_bi": (i, [vp, vp, vp, vp, i, i, i, vp]),
             "ak_silu_mul": (i, [vp, vp, i, i, vp]),
             "ak_wq_gemv_kt_silu": (i, [i, vp, i, vp, vp, vp, i, i, i, i, vp]),

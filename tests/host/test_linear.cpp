@@ -108,8 +108,11 @@ int main() {
       std::memcpy(&f, &u, 4);
       return (double)f;
     };
-    for (size_t tile : {(size_t)64 << 20, (size_t)256 * k * 2}) {
-      set_prefill_tile_bytes(tile);
+    // routes: dequantized tiles (one tile, tiles of 256 rows) x library GEMM, then the fused GEMM (two parts of
+    // different bits into one output)
+    for (int route = 0; route < 3; ++route) {
+      set_prefill_route(route < 2 ? 0 : 1);
+      set_prefill_tile_bytes(route == 1 ? (size_t)256 * k * 2 : (size_t)64 << 20);
       EXPECT(linear(gu, x.ptr(), y.ptr(), m, n, k, 0, nullptr) == 0, "prefill linear");
       const auto hy = get(y.ptr(), (size_t)m * n);
       int bad = 0;
@@ -126,6 +129,7 @@ int main() {
       EXPECT(bad == 0, "prefill linear == dequantized weights x x");
     }
     set_prefill_tile_bytes((size_t)64 << 20);
+    set_prefill_route(-1);
   }
   // ---- linear_shared: three single-part linears of mixed bits sharing x (two classes: W3 and W4)
   std::vector<uint8_t> pa, sa, pb, sb, pc, sc;

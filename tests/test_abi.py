@@ -65,6 +65,11 @@ def test_invalid_arguments_return_1_without_a_gpu(K):
     assert K.ak_bf16_gemv_bi(one, one, None, one, 129, 16, 1024, None) == 1
     assert K.ak_bf16_gemv_bi_ld(one, one, None, one, 1, 16, 1040, 16, None) == 1
     assert K.ak_bf16_gemv_bi_ld(one, one, None, one, 2, 16, 1024, 15, None) == 1  # ldy < n: token rows overlap
+    # the fused prefill GEMM: bits, ldy < n, k % group, m < 1 -> 1 (before any device call)
+    assert K.ak_wq_gemm_kt(5, one, 1, one, one, one, 16, 0, 1024, 128, None) == 1
+    assert K.ak_wq_gemm_kt(4, one, 1, one, one, one, 16, 8, 1024, 128, None) == 1
+    assert K.ak_wq_gemm_kt(4, one, 1, one, one, one, 16, 0, 1000, 128, None) == 1
+    assert K.ak_wq_gemm_kt(4, one, 0, one, one, one, 16, 0, 1024, 128, None) == 1
     # the no-alloc GEMV refuses a call whose worst-case split-K scratch, 4096 + 64 * P * T * sum(ceil(n / 16)) bytes,
     # exceeds its 64 MiB static array (here 8 * 16 * 8750 blocks), before any device call
     ns = (ctypes.c_int * 1)(140000)
