@@ -12,6 +12,7 @@
 #include <new>
 
 #include "agens_kernels.h"
+#include "agens_tuning.h"
 #include "wq_common.h"
 
 namespace agq {
@@ -25,6 +26,8 @@ int m1d_chain_make(int nsteps, const int* bits, const void* const* x, const int*
                    const int* wait, const int* act, void** table, int* mt_out, size_t* smem_out);
 int m1d_chain_launch(const void* table, int nsteps, int mt, size_t smem, hipStream_t s);
 int m1d_chain_error(int* err);
+void m1d_tune_override(int split, int nwv, int sk);
+int m1d_tune_query(int bits, int m, const Segs& g, int k, int* split, int* nwv, int* sk);
 
 namespace {
 
@@ -367,6 +370,20 @@ int ak_wq_chain_status(void) {
   int err = 0;
   const int e = m1d_chain_error(&err);
   return e ? -e : err;
+}
+
+int ak_wq_tune_override(int split, int nwv, int sk) {
+  m1d_tune_override(split, nwv, sk < -2 ? -1 : sk > 1 ? 1 : sk);
+  return 0;
+}
+
+int ak_wq_tune_query(int bits, int m, int nseg, const int* n, int k, int* split, int* nwv, int* sk) {
+  if (!n || !split || !nwv || !sk || nseg < 1 || nseg > kMaxSegs || !group_ok(k, 128)) return AK_INVALID;
+  for (int i = 0; i < nseg; ++i)
+    if (n[i] < 1) return AK_INVALID;
+  void* dummy[kMaxSegs] = {};
+  const Segs g = make_segs(nseg, dummy, dummy, dummy, n, nullptr, 16);
+  return m1d_tune_query(bits, m, g, k, split, nwv, sk);
 }
 
 int ak_w4_set_mma(int mode) {

@@ -552,6 +552,43 @@ struct M1dShape {
   size_t smem;
 };
 
+// ---- launch configurations pinned by measurement (wq_launch_table.h, written by tune_launch.py) and the tuner's
+// override.  A pin names a shape -- bits, padded tokens, k, the segments' rows -- and the stripe sets per block
+// (split), waves per workgroup (nwv) and split-K across workgroups (sk) measured fastest for it, and the fastest split
+// with 16 waves (csplit: a chained launch always has 16); every configuration gives the same bits, so a pin changes
+// only the speed.  Shapes without a pin take the cost model below.
+struct M1dPin {
+  int bits, mt, k, nseg, n[4];
+  int split, nwv, sk, csplit;
+};
+#include "wq_launch_table.h"
+
+struct TuneOverride {
+  int split = 0, nwv = 0, sk = -1;  // 0 / -1: not overridden
+  bool nopins = false;              // the cost model alone (the tuner's reference)
+};
+TuneOverride g_tune;
+
+const M1dPin* find_pin(const I8Args& a, int bits, int mt) {
+  if (g_tune.nopins) return nullptr;
+  const Segs& g = a.segs;
+  for (int i = 0; i < (int)(sizeof(kM1dPins) / sizeof(kM1dPins[0])); ++i) {
+    const M1dPin& p = kM1dPins[i];
+    if (p.bits != bits || p.mt != mt || p.k != a.k || p.nseg != g.nseg) continue;
+    bool same = true;
+    for (int j = 0; j < g.nseg; ++j) same = same && p.n[j] == g.n[j];
+    if (same) return &p;
+  }
+  return nullptr;
+}
+
+// split-K across workgroups: -1 the default rule (wherever the shape suits it), 0 no, 1 yes
+int m1d_sk_choice(const I8Args& a, int bits, int mt) {
+  if (g_tune.sk >= 0) return g_tune.sk;
+  const M1dPin* p = find_pin(a, bits, mt);
+  return p && p->sk >= 0 ? p->sk : -1;
+}
+
 int plan_m1d(I8Args& a, int bits, int mt, bool chain, M1dShape& sh) {
   const Segs& g = a.segs;
   const size_t x_bytes = m1d_x_bytes(a.nquad, mt);
@@ -598,6 +635,17 @@ int plan_m1d(I8Args& a, int bits, int mt, bool chain, M1dShape& sh) {
     }
   }
   if (best > 1e29) return AK_INVALID;
+  // a measured pin (or the tuner's override) replaces the model's choice where the shape admits it
+  const M1dPin* pin = find_pin(a, bits, mt);
+  // (csplit 0: a chained launch keeps the model's split)
+  const int want_split = g_tune.split ? g_tune.split : pin ? (chain ? pin->csplit : pin->split) : 0;
+  const int want_nwv = g_tune.nwv ? g_tune.nwv : pin ? pin->nwv : 0;
+  if (want_split || want_nwv) {
+    const int sp = want_split ? want_split : best_split, nw = chain ? 16 : want_nwv ? want_nwv : best_nwv;
+    const bool ok = (sp == 1 || sp == 2 || sp == 4 || sp == 8) && sp <= a.P && (nw == 16 || nw == 8) &&
+                    x_bytes + (size_t)nbmax * m1d_block_bytes(a.P, sp, mt) + 16 <= 160 * 1024;
+    if (ok) best_split = sp, best_nwv = nw;
+  }
   sh.split = best_split;
   sh.nwv = best_nwv;
   sh.grid = grid;
@@ -623,7 +671,9 @@ void launch_split(const I8Args& a, int grid, int nwv, size_t smem, hipStream_t s
 // false if the launch does not suit it
 bool m1d_sk_shape(const I8Args& a, int bits, int mt, int* nr_out, size_t* smem_out, size_t* scratch_out) {
   const Segs& g = a.segs;
-  if (mt > 2 || g.nseg != 1 || a.P != 8 || a.nquad < AK_M1_SK_QUADS) return false;
+  const int choice = m1d_sk_choice(a, bits, mt);
+  if (choice == 0) return false;
+  if (mt > 2 || g.nseg != 1 || a.P != 8 || (a.nquad < AK_M1_SK_QUADS && choice != 1)) return false;
   if ((long long)(a.nquad / 2) * g.n[0] * 128 * bits >= (1ll << 31)) return false;
   const int cus = num_cus(), nr = cus / a.P, nb4 = (g.n[0] + 3) / 4, nbr = nr > 0 ? (nb4 + nr - 1) / nr : 0;
   int nqs = 0;
@@ -837,6 +887,40 @@ int m1d_chain_launch(const void* table, int nsteps, int mt, size_t smem, hipStre
   else
     hipLaunchKernelGGL(i8_chain_kernel<2>, dim3(num_cus()), dim3(1024), smem, s, t, nsteps);
   return (int)hipGetLastError();
+}
+
+// the tuner's override of the launch configuration (0 / -1: the pins and the model)
+void m1d_tune_override(int split, int nwv, int sk) {
+  g_tune.nopins = sk == -2;
+  g_tune.split = split;
+  g_tune.nwv = nwv;
+  g_tune.sk = sk < -1 ? -1 : sk;
+}
+
+// the configuration a one- or two-token launch of this shape takes: split, nwv, sk (1 split-K across workgroups)
+int m1d_tune_query(int bits, int m, const Segs& g, int k, int* split, int* nwv, int* sk) {
+  if (m < 1 || m > 2 || bits < 2 || bits > 4) return AK_INVALID;
+  I8Args a;
+  a.segs = g;
+  a.x = nullptr;
+  a.m = m;
+  a.k = k;
+  a.nquad = kpad(k) / kG / 4;
+  a.qpt = 2;
+  a.P = stripe_count(a.nquad, a.qpt);
+  a.nb = 0;
+  a.part = nullptr;
+  a.cnt = nullptr;
+  int nr = 0;
+  size_t smem = 0, zb = 0;
+  if (m1d_sk_shape(a, bits, m, &nr, &smem, &zb)) {
+    *split = 1, *nwv = 16, *sk = 1;
+    return 0;
+  }
+  M1dShape sh;
+  if (plan_m1d(a, bits, m, false, sh)) return AK_INVALID;
+  *split = sh.split, *nwv = sh.nwv, *sk = 0;
+  return 0;
 }
 
 // reads and clears the flag a chained launch raises when a wait ran out (0.2 s): 1 if one did since the last call

@@ -187,8 +187,9 @@ def max_ulp_bound(y_bits, ref64, mag):
 
 # ------------------------------------------------------------------------------------------------ product library
 def header_symbols():
-    """Function names declared in include/agens_kernels.h."""
-    txt = open(HEADER).read()
+    """Function names declared in include/*.h (the C ABI and its tuning entry points)."""
+    inc = os.path.dirname(HEADER)
+    txt = "".join(open(os.path.join(inc, f)).read() for f in sorted(os.listdir(inc)) if f.endswith(".h"))
     txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
     return sorted(set(re.findall(r"\b(ak_\w+)\s*\(", txt)))
 

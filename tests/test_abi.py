@@ -106,3 +106,38 @@ def test_chain_invalid_arguments_return_1_without_a_gpu(K):
     assert K.ak_wq_chain_create(st, 1, ctypes.byref(h)) == 1
     assert K.ak_wq_chain_run(None, None) == 1
     assert K.ak_wq_chain_destroy(None) == 0
+
+
+def test_launch_table_pins_are_honoured(K):
+    """Every shape pinned in csrc/wq_launch_table.h (written by tune_launch.py from measurements) is launched with its
+    pinned configuration (ak_wq_tune_query, no device needed), and the tuner's override takes precedence until
+    cleared.  The bits do not depend on the configuration (the GPU parity tests and the tuner check that)."""
+    import ctypes
+    import os
+    import re
+    ci = ctypes.c_int
+    K.ak_wq_tune_query.argtypes = [ci, ci, ci, ctypes.POINTER(ci), ci, ctypes.POINTER(ci), ctypes.POINTER(ci),
+                                   ctypes.POINTER(ci)]
+    K.ak_wq_tune_override.argtypes = [ci, ci, ci]
+    tab = open(os.path.join(os.path.dirname(KERNELS_SO), "csrc", "wq_launch_table.h")).read()
+    num = r"(-?\d+)"
+    pins = re.findall(r"\{" + ", ".join([num] * 4) + r", \{" + ", ".join([num] * 4) + r"\}, " + ", ".join([num] * 4) + r"\}", tab)
+    got = [ci(), ci(), ci()]
+    for p in pins:
+        bits, m, k, nseg, n0, n1, n2, n3, split, nwv, sk, csplit = (int(v) for v in p)
+        if bits == 0:
+            continue
+        ns = (ci * 4)(n0, n1, n2, n3)
+        assert K.ak_wq_tune_query(bits, m, nseg, ns, k, *[ctypes.byref(g) for g in got]) == 0
+        want = (1, 16, 1) if sk == 1 else (split, nwv, 0)
+        assert tuple(g.value for g in got) == want, (p, [g.value for g in got])
+    # the override wins, and clearing it restores the plan
+    ns = (ci * 4)(5120, 0, 0, 0)
+    assert K.ak_wq_tune_query(3, 1, 1, ns, 5120, *[ctypes.byref(g) for g in got]) == 0
+    before = tuple(g.value for g in got)
+    K.ak_wq_tune_override(2, 8, 0)
+    assert K.ak_wq_tune_query(3, 1, 1, ns, 5120, *[ctypes.byref(g) for g in got]) == 0
+    assert tuple(g.value for g in got) == (2, 8, 0)
+    K.ak_wq_tune_override(0, 0, -1)
+    assert K.ak_wq_tune_query(3, 1, 1, ns, 5120, *[ctypes.byref(g) for g in got]) == 0
+    assert tuple(g.value for g in got) == before
