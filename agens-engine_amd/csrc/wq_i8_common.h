@@ -130,21 +130,26 @@ __device__ __forceinline__ float group_sum_f32(const i32x4& d) {
 // The activation scale of a group as fp32 bits, from the group's largest bf16 magnitude pattern mx (sign cleared):
 // 2^(E - 148) with E = mx >> 7 the largest exponent field; a group holding a NaN (mx above the Inf pattern 0x7F80):
 // NaN; a group holding an Inf but no NaN: +Inf.  In a non-finite group every finite input converts to 0 and every Inf
-// to its sign (+-1, see clamp_nonfinite), so the group sum S is the sum of sign(x) * q over the Inf inputs and the
+// to its sign (+-1, see x_int), so the group sum S is the sum of sign(x) * q over the Inf inputs and the
 // group adds S * scale * Inf: +-Inf, or NaN where S = 0 -- the fp32 path's value wherever the group's Inf products
 // share one sign (the fp32 path gives NaN for products of both signs, where S may be nonzero).
 __device__ __forceinline__ int act_scale_bits(int mx) {
   return mx > 0x7F80 ? 0x7FC00000 : mx == 0x7F80 ? 0x7F800000 : __float_as_int(ldexpf(1.0f, (mx >> 7) - 148));
 }
 
-// x_int of a non-finite group (E = 255): trunc(x * 2^-107) is 0 for every finite bf16, the conversion saturates for
-// +-Inf and gives 0 for NaN; clamped to [-1, 1] that is sign(x) for an Inf and 0 otherwise.  A finite group is left
-// as it is (the branch is skipped when no lane of the wave holds a non-finite group).
-__device__ __forceinline__ void clamp_nonfinite(int e, int (&xi)[8]) {
-  if (e == 255) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) xi[i] = min(max(xi[i], -1), 1);
-  }
+// x_int of one bf16 input of a group with largest exponent field e: trunc(x * 2^(148 - e)), exact (|x_int| < 2^22).
+// A non-finite group (e = 255): +-1 for +-Inf and 0 for every finite input (scaled by 2^-200 instead, every finite bf16
+// truncates to 0, an Inf stays infinite and is clamped to its sign); a NaN group's values do not matter, its activation
+// scale is NaN.  XiScale holds the group's exponent shift and clamp bound.
+struct XiScale {
+  int sh;
+  float lim;
+};
+__device__ __forceinline__ XiScale xi_scale(int e) {
+  return e == 255 ? XiScale{-200, 1.0f} : XiScale{148 - e, 16777216.0f};
+}
+__device__ __forceinline__ int x_int(uint32_t b16, XiScale s) {
+  return (int)__builtin_amdgcn_fmed3f(ldexpf(bf2f(b16), s.sh), -s.lim, s.lim);
 }
 
 // Reductions over aligned groups of L lanes (L = 2, 4, 8 or 16) with DPP: two quad swaps, then the half-row and the
@@ -159,18 +164,6 @@ __device__ __forceinline__ int dpp_group_reduce(int v) {
   return v;
 }
 
-// Sum of the signed bytes j of t[0..7] (one limb of eight inputs): packed four at a time, then dot products with ones
-__device__ __forceinline__ int limb_sum8(const uint32_t (&t)[8], int j) {
-  const uint32_t sel = (uint32_t)j | ((uint32_t)(4 + j) << 8) | 0x0C0C0000u;  // [a.byte j, b.byte j, 0, 0]
-  int s = 0;
-#pragma unroll
-  for (int i = 0; i < 8; i += 4) {
-    const uint32_t lo = __builtin_amdgcn_perm(t[i + 1], t[i], sel), hi = __builtin_amdgcn_perm(t[i + 3], t[i + 2], sel);
-    s = __builtin_amdgcn_sdot4((int)(lo | (hi << 16)), 0x01010101, s, false);
-  }
-  return s;
-}
-
 // One group's activation limbs from 8 consecutive bf16 inputs per lane, LPU lanes per group: the group's largest
 // magnitude pattern mx (all LPU lanes; the exponent field E = mx >> 7) and, per input, x_int = trunc(x * 2^(148 - E))
 // with its three limb-byte sources.
@@ -181,19 +174,13 @@ __device__ __forceinline__ int group_limbs(const uint4 v, uint32_t (&t0)[8], uin
 #pragma unroll
   for (int i = 0; i < 4; ++i) mx = max(mx, max((int)(w[i] & 0x7FFFu), (int)((w[i] >> 16) & 0x7FFFu)));
   mx = dpp_group_reduce<LPU, true>(mx);
-  const int e = mx >> 7;
-  int xi[8];
+  const XiScale xs = xi_scale(mx >> 7);
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const uint32_t b16 = (w[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
-    xi[i] = (int)ldexpf(bf2f(b16), 148 - e);  // exact; truncation toward zero
-  }
-  clamp_nonfinite(e, xi);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    t0[i] = (uint32_t)xi[i];          // limb 0 = byte 0
-    t1[i] = (uint32_t)xi[i] + 0x80u;    // limb 1 = byte 1
-    t2[i] = (uint32_t)xi[i] + 0x8080u;  // limb 2 = byte 2
+    const int xi = x_int((w[i >> 1] >> (16 * (i & 1))) & 0xFFFFu, xs);
+    t0[i] = (uint32_t)xi;          // limb 0 = byte 0
+    t1[i] = (uint32_t)xi + 0x80u;    // limb 1 = byte 1
+    t2[i] = (uint32_t)xi + 0x8080u;  // limb 2 = byte 2
   }
   return mx;
 }
@@ -242,17 +229,43 @@ __device__ __forceinline__ void store_limbs(uint8_t* dst, size_t half_stride, in
 
 
 
-// One unit of a group-128 activation image: a group of 128 inputs of one token held by 16 lanes, 8 consecutive inputs
-// each (o0 = the lane's first input within its 32-input lane chunk).  Computes what group_limbs, store_limbs and the
-// limb sums do, with fewer operations:
+// The inputs a lane converts.  A unit is a group of 128 inputs of one token held by 16 lanes (sub = lane of the group,
+// chunk sub / 4 of the group, lq = sub % 4 within the chunk); each lane holds four pairs of adjacent inputs, pair c
+// (c < 4) at element offset unit_pair_offset(sub, c) of the group.  The pairs are chosen so that a lane's limb bytes
+// fill whole dwords of the MFMA A operand, whose input order follows make_b:
+//   W4: 8 consecutive inputs 8 lq .. 8 lq + 7 (even inputs -> half 0, odd -> half 1, dword lq of each);
+//   W3: inputs 8 c + 2 lq (+1): half lq / 2, dwords 2 (lq % 2) (low input of each pair) and +1 (high), byte c;
+//   W2: inputs 16 (lq / 2) + 2 (lq % 2) + 4 c (+1): the same half, dwords and bytes.
+template <int BITS>
+__device__ __forceinline__ int unit_pair_offset(int sub, int c) {
+  const int l = sub & 3, base = 32 * (sub >> 2);
+  return BITS == 4 ? base + 8 * l + 2 * c : BITS == 3 ? base + 2 * l + 8 * c : base + 16 * (l >> 1) + 2 * (l & 1) + 4 * c;
+}
+// the lane's four pairs of the group starting at g (generic pointer)
+template <int BITS>
+__device__ __forceinline__ uint4 load_unit(const uint16_t* g, int sub) {
+  if constexpr (BITS == 4) {
+    return *reinterpret_cast<const uint4*>(g + unit_pair_offset<4>(sub, 0));
+  } else {
+    uint32_t w[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) w[c] = *reinterpret_cast<const uint32_t*>(g + unit_pair_offset<BITS>(sub, c));
+    return make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+// One unit of a group-128 activation image (the lane's pairs in v, as load_unit gives them): computes what
+// group_limbs, store_limbs and the limb sums do, with fewer operations:
 //   - the group's largest exponent field is the exponent of the largest magnitude (packed 16-bit maxima of the sign-
 //     cleared patterns; NaN / Inf patterns order above every finite one, as their exponent fields do);
-//   - W4: the limb dwords are gathered with byte permutes and their sums taken from the same dwords (sdot4);
+//   - the limb dwords are gathered with byte permutes, their sums taken from the same dwords (sdot4), and written
+//     whole (W4: one dword per half and limb; W2 / W3: one 8-byte store per limb);
 //   - the limb-0 and limb-1 sums of the group share one packed reduction (|sum| <= 128 * 128 < 2^15).
-// Returns the group's largest magnitude pattern (act_scale_bits' argument); d0..d2 = the group's limb sums (every lane
-// of the unit).  store = false: nothing is written.
+// dst points at (chunk, half 0, limb 0) of the LDS operand layout (limb rows 16 bytes apart), half_stride = bytes
+// between half 0 and half 1.  Returns the group's largest magnitude pattern (act_scale_bits' argument); d0..d2 = the
+// group's limb sums (every lane of the unit).  store = false: nothing is written.
 template <int BITS>
-__device__ __forceinline__ int convert_unit(const uint4 v, uint8_t* dst, size_t half_stride, int o0, bool store,
+__device__ __forceinline__ int convert_unit(const uint4 v, uint8_t* dst, size_t half_stride, int lq, bool store,
                                             int& d0, int& d1, int& d2) {
   typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
   auto mag = [](uint32_t w) {
@@ -261,49 +274,44 @@ __device__ __forceinline__ int convert_unit(const uint4 v, uint8_t* dst, size_t 
   };
   const u16x2 mx = __builtin_elementwise_max(__builtin_elementwise_max(mag(v.x), mag(v.y)),
                                              __builtin_elementwise_max(mag(v.z), mag(v.w)));
-  const int mxg = dpp_group_reduce<16, true>(max((int)mx.x, (int)mx.y)), e = mxg >> 7;
+  const int mxg = dpp_group_reduce<16, true>(max((int)mx.x, (int)mx.y));
+  const XiScale xs = xi_scale(mxg >> 7);
   const uint32_t w[4] = {v.x, v.y, v.z, v.w};
   uint32_t t0[8], t1[8], t2[8];
-  int xi[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const uint32_t b16 = (w[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
-    xi[i] = (int)ldexpf(bf2f(b16), 148 - e);  // exact; truncation toward zero
+    const int xi = x_int((w[i >> 1] >> (16 * (i & 1))) & 0xFFFFu, xs);
+    t0[i] = (uint32_t)xi;
+    t1[i] = (uint32_t)xi + 0x80u;
+    t2[i] = (uint32_t)xi + 0x8080u;
   }
-  clamp_nonfinite(e, xi);
+  int sums[3];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    t0[i] = (uint32_t)xi[i];
-    t1[i] = (uint32_t)xi[i] + 0x80u;
-    t2[i] = (uint32_t)xi[i] + 0x8080u;
-  }
-  int s0 = 0, s1 = 0, s2 = 0;
-  if constexpr (BITS == 4) {
-    // word o0 / 8 of each limb row: even inputs -> half 0, odd -> half 1
-    const int v4 = o0 >> 3;
+  for (int limb = 0; limb < 3; ++limb) {
+    const uint32_t* t = limb == 0 ? t0 : limb == 1 ? t1 : t2;
+    const uint32_t sel = (uint32_t)limb | ((uint32_t)(4 + limb) << 8) | 0x0C0C0000u;  // [a.byte l, b.byte l, 0, 0]
+    // W4: half hf = inputs hf, hf + 2, hf + 4, hf + 6; W2 / W3: dword 0 = the pairs' low inputs 0, 2, 4, 6, dword 1 =
+    // their high inputs: the same two gathers
+    uint32_t d[2];
 #pragma unroll
-    for (int limb = 0; limb < 3; ++limb) {
-      const uint32_t* t = limb == 0 ? t0 : limb == 1 ? t1 : t2;
-      const uint32_t sel = (uint32_t)limb | ((uint32_t)(4 + limb) << 8) | 0x0C0C0000u;  // [a.byte l, b.byte l, 0, 0]
-      int s = 0;
-#pragma unroll
-      for (int hf = 0; hf < 2; ++hf) {
-        const uint32_t lo = __builtin_amdgcn_perm(t[hf + 2], t[hf], sel);
-        const uint32_t hi = __builtin_amdgcn_perm(t[hf + 6], t[hf + 4], sel);
-        const uint32_t d = lo | (hi << 16);
-        s = __builtin_amdgcn_sdot4((int)d, 0x01010101, s, false);
-        if (store) *reinterpret_cast<uint32_t*>(dst + hf * half_stride + limb * 16 + 4 * v4) = d;
-      }
-      (limb == 0 ? s0 : limb == 1 ? s1 : s2) = s;
+    for (int hf = 0; hf < 2; ++hf) {
+      const uint32_t lo = __builtin_amdgcn_perm(t[hf + 2], t[hf], sel);
+      const uint32_t hi = __builtin_amdgcn_perm(t[hf + 6], t[hf + 4], sel);
+      d[hf] = lo | (hi << 16);
     }
-  } else {
-    s0 = limb_sum8(t0, 0);
-    s1 = limb_sum8(t1, 1);
-    s2 = limb_sum8(t2, 2);
-    if (store) store_limbs<BITS>(dst, half_stride, o0, t0, t1, t2);
+    sums[limb] = __builtin_amdgcn_sdot4((int)d[1], 0x01010101, __builtin_amdgcn_sdot4((int)d[0], 0x01010101, 0, false),
+                                        false);
+    if (store) {
+      if constexpr (BITS == 4) {
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) *reinterpret_cast<uint32_t*>(dst + hf * half_stride + limb * 16 + 4 * lq) = d[hf];
+      } else {
+        *reinterpret_cast<uint2*>(dst + (lq >> 1) * half_stride + limb * 16 + 8 * (lq & 1)) = make_uint2(d[0], d[1]);
+      }
+    }
   }
-  const int p01 = dpp_group_reduce<16, false>(s0 + (int)((uint32_t)s1 << 16));
-  d2 = dpp_group_reduce<16, false>(s2);
+  const int p01 = dpp_group_reduce<16, false>(sums[0] + (int)((uint32_t)sums[1] << 16));
+  d2 = dpp_group_reduce<16, false>(sums[2]);
   d0 = (int)(short)(p01 & 0xFFFF);
   d1 = (p01 - d0) >> 16;
   return mxg;

@@ -239,23 +239,31 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
   auto xload = [&](int pass0) {
 #pragma unroll
     for (int b = 0; b < XB; ++b) {
-      // lanes past the end load x[0] (zero-selected); passes past npass load nothing (a wave-uniform branch)
-      const int u = u0 + (pass0 + b) * ustride, t = MT == 1 ? 0 : u / gpt, kk = (4 * q0 + u - t * gpt) * kG + 8 * sub;
-      const bool ok = u < units && t < mm && kk < k;
+      // lanes past the end load from x[0] (zero-selected); passes past npass load nothing (a wave-uniform branch)
+      const int u = u0 + (pass0 + b) * ustride, t = MT == 1 ? 0 : u / gpt, gk = (4 * q0 + u - t * gpt) * kG;
+      const bool ok = u < units && t < mm && gk < k;
       xv[b] = make_uint4(0u, 0u, 0u, 0u);
       if (pass0 + b < npass) {
-        const int xo = ok ? t * xk + kk : 0;
+        const int xo = ok ? t * xk + gk : 0;  // the unit's group
         if constexpr (CHAIN) {  // device-coherent: x may be an earlier step's output, written by another XCD
-          const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rx, xo * 2, 0, kSc1);
-          uint4 g = make_uint4(v[0], v[1], v[2], v[3]);
-          if (act) {
-            const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rx, (xo + k) * 2, 0, kSc1);
-            g = silu_mul8(g, make_uint4(w[0], w[1], w[2], w[3]));
-          }
+          auto ld = [&](int o) {
+            if constexpr (BITS == 4) {
+              const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rx, (o + unit_pair_offset<4>(sub, 0)) * 2, 0, kSc1);
+              return make_uint4(v[0], v[1], v[2], v[3]);
+            } else {
+              uint32_t v[4];
+#pragma unroll
+              for (int c = 0; c < 4; ++c)
+                v[c] = __builtin_amdgcn_raw_buffer_load_b32(rx, (o + unit_pair_offset<BITS>(sub, c)) * 2, 0, kSc1);
+              return make_uint4(v[0], v[1], v[2], v[3]);
+            }
+          };
+          uint4 g = ld(xo);
+          if (act) g = silu_mul8(g, ld(xo + k));
           xv[b] = ok ? g : make_uint4(0u, 0u, 0u, 0u);
         } else {
-          uint4 g = *reinterpret_cast<const uint4*>(a.x + xo);
-          if (act) g = silu_mul8(g, *reinterpret_cast<const uint4*>(a.x + xo + k));
+          uint4 g = load_unit<BITS>(a.x + xo, sub);
+          if (act) g = silu_mul8(g, load_unit<BITS>(a.x + xo + k, sub));
           xv[b] = ok ? g : make_uint4(0u, 0u, 0u, 0u);
         }
       }
@@ -350,7 +358,7 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
       const int t = MT == 1 || !live ? 0 : u / gpt, ut = live ? u - t * gpt : 0;
       const int qd = ut >> 2, gq = ut & 3, eg0 = 8 * sub, cqd = gq * 4 + (eg0 >> 5);
       int b0, b1, b2;
-      const int e = convert_unit<BITS>(xv[b], xq + t * tstride + qd * kCPQ * 96 + cqd * 48, kCPQ * 48, eg0 & 31, live,
+      const int e = convert_unit<BITS>(xv[b], xq + t * tstride + qd * kCPQ * 96 + cqd * 48, kCPQ * 48, sub & 3, live,
                                        b0, b1, b2);
       if (live) {
         if (sub == 0) {

@@ -192,13 +192,13 @@ __global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
   auto xload = [&](int pass0) {
 #pragma unroll
     for (int b = 0; b < XB; ++b) {
-      const int u = u0 + (pass0 + b) * ustride, t = u / cg, kk = (g0 + u - t * cg) * kG + 8 * sub;
-      const bool ok = u < units && t < mm && kk < k;
+      const int u = u0 + (pass0 + b) * ustride, t = u / cg, gk = (g0 + u - t * cg) * kG;
+      const bool ok = u < units && t < mm && gk < k;
       xv[b] = make_uint4(0u, 0u, 0u, 0u);
       if (pass0 + b < npass) {
-        const size_t xo = ok ? (size_t)t * (ACT ? 2 * k : k) + kk : 0;
-        uint4 v = *reinterpret_cast<const uint4*>(xb + xo);
-        if constexpr (ACT) v = silu_mul8(v, *reinterpret_cast<const uint4*>(xb + xo + k));
+        const size_t xo = ok ? (size_t)t * (ACT ? 2 * k : k) + gk : 0;  // the unit's group
+        uint4 v = load_unit<BITS>(xb + xo, sub);
+        if constexpr (ACT) v = silu_mul8(v, load_unit<BITS>(xb + xo + k, sub));
         xv[b] = ok ? v : make_uint4(0u, 0u, 0u, 0u);
       }
     }
@@ -282,7 +282,7 @@ __global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
       const int eg0 = 8 * sub, ch = eg0 >> 5;
       int b0, b1, b2;
       const int e = convert_unit<BITS>(xv[b], ximg + ((g * 2) * NT + tg) * 768 + ch * 192 + ui * 48, NT * 768,
-                                       eg0 & 31, live, b0, b1, b2);
+                                       sub & 3, live, b0, b1, b2);
       if (live) {
         if (sub == 0) {
           constexpr int OFF = code_offset<BITS>();

@@ -22,7 +22,7 @@ from _lib import (kernels, check, Dev, Linear, gemv, gen_container, gen_scales, 
 
 pytestmark = pytest.mark.gpu
 
-PINF, NINF, QNAN = 0x7F80, 0xFF80, 0x7FC0
+PINF, NINF, QNAN, BIG = 0x7F80, 0xFF80, 0x7FC0, 0x7680  # BIG = 2^110
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -37,14 +37,17 @@ def gpu():
 
 
 def special_x(m, k, group, seed):
-    """m tokens: token t % 4 == 0: one +Inf in group 1; 1: a NaN in group 2; 2: -Inf in group 0 and +Inf in the last
+    """m tokens: token t % 4 == 0: one +Inf and one finite 2^110 in group 1 (x * 2^-107 would truncate to 8; the finite
+    input must count 0); 1: a NaN in group 2; 2: -Inf in group 0 and +Inf in the last
     group; 3: every input subnormal (bf16 exponent field 0); the rest of each token N(0, 1)."""
     x = gen_x(seed, m * k).reshape(m, k)
     rng = np.random.default_rng(seed)
     for t in range(m):
         r = t % 4
         if r == 0:
-            x[t, group + int(rng.integers(group))] = PINF
+            i = int(rng.integers(group))
+            x[t, group + i] = PINF
+            x[t, group + (i + 1 + int(rng.integers(group - 1))) % group] = BIG  # finite, counts 0 beside the Inf
         elif r == 1:
             x[t, 2 * group + int(rng.integers(group))] = QNAN
         elif r == 2:
