@@ -17,6 +17,10 @@ struct I8Args {
   float* part;    // split-K launches: stripe partials [P][tokens][rows] and, at cnt, one counter per row range
   int* cnt;
   int act = 0;    // 1: x is the merged gate_up [m][2k] and the activations are SiLU(gate) * up (wq_silu.h)
+  // group-128 kernels (set_tile_stripes): the multiplier of x / P (0 for P = 1) and bit t set when 1024-input tile t
+  // ends a stripe (up to 64 tiles)
+  unsigned pmul = 0;
+  unsigned long long ends = 0;
 };
 
 // The P (<= 8) stripe partials of one output of a split-K launch, at float offsets off + q * stride (q < P) of base,
@@ -42,14 +46,28 @@ __host__ __device__ inline int stripe_count(int nquad, int qpt) { return nquad /
 // x / d for 0 <= x < 2^23 and 1 <= d <= 8 by a multiply with ceil(2^32 / d) (exact in that range: the error term
 // x (M d - 2^32) / (d 2^32) < 2^-9 stays below the distance 1 / d of x / d to the next integer); a runtime 32-bit
 // division is a long instruction sequence on the GPU, and the scalar unit running it is shared by the CU's waves
+__host__ __device__ inline unsigned upto8_mul(int d) {
+  return d == 2 ? 2147483649u : d == 3 ? 1431655766u : d == 4 ? 1073741825u : d == 5 ? 858993460u
+       : d == 6 ? 715827883u : d == 7 ? 613566757u : 536870913u;
+}
 __host__ __device__ inline int div_upto8(int x, int d) {
-  const unsigned m = d == 2 ? 2147483649u : d == 3 ? 1431655766u : d == 4 ? 1073741825u : d == 5 ? 858993460u
-                   : d == 6 ? 715827883u : d == 7 ? 613566757u : 536870913u;
-  return d == 1 ? x : (int)(((unsigned long long)(unsigned)x * m) >> 32);
+  return d == 1 ? x : (int)(((unsigned long long)(unsigned)x * upto8_mul(d)) >> 32);
 }
 // first quad of stripe p (p <= P <= 8, fewer than 2^20 tiles)
 __host__ __device__ inline int stripe_begin(int p, int nquad, int P, int qpt) {
   return qpt * div_upto8(p * (nquad / qpt), P);
+}
+// x / P with the launch's multiplier (branch-free on the device: a selection on P costs scalar branches)
+__device__ __forceinline__ int div_by_p(int x, const I8Args& a) {
+  return (int)(((unsigned long long)(unsigned)x * a.pmul) >> 32) + (a.P == 1 ? x : 0);
+}
+// P, its multiplier and the stripe-end mask of a group-128 launch (qpt 2) from nquad
+inline void set_tile_stripes(I8Args& a) {
+  a.P = stripe_count(a.nquad, 2);
+  a.pmul = a.P == 1 ? 0u : upto8_mul(a.P);
+  const int nt = a.nquad / 2;
+  a.ends = 0;
+  for (int p = 0; p < a.P && nt <= 64; ++p) a.ends |= 1ull << (stripe_begin(p + 1, a.nquad, a.P, 2) / 2 - 1);
 }
 
 namespace {

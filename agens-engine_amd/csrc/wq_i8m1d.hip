@@ -173,6 +173,7 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
   const int P = a.P, nquad = a.nquad, k = a.k, mm = a.m;  // mm <= MT tokens (the others are zero, not written)
   const int ntile = nquad >> 1;
   const int nwv = CHAIN ? 16 : blockDim.x >> 6;  // a chained launch has 16 waves
+  const int lg_nwv = CHAIN ? 4 : __builtin_ctz((unsigned)nwv);  // 8 or 16 waves: divisions by shifts
   int tid = threadIdx.x;
   // chained: an opaque thread index per step, so that nothing lane-dependent is hoisted out of the step loop (the
   // hoisted values would stay live across every step's item loop)
@@ -195,13 +196,16 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
   int sg = 0;
 #pragma unroll
   for (int i = 1; i < kMaxSegs; ++i) sg += (i < sgs.nseg && (int)blockIdx.x >= a.wg_end[i - 1]) ? 1 : 0;
-  const int nr = SK ? a.wg_end[0] / P : 1, r = SK ? (int)blockIdx.x / P : 0, psk = SK ? (int)blockIdx.x - r * P : 0;
+  const int nr = SK ? div_by_p(a.wg_end[0], a) : 1, r = SK ? div_by_p((int)blockIdx.x, a) : 0;
+  const int psk = SK ? (int)blockIdx.x - r * P : 0;
+  // first tile of stripe p (the launch's multiplier: no scalar branches on P)
+  auto stripe_tile = [&](int p) { return div_by_p(p * ntile, a); };
   const int wg0 = sg ? AK_PICK(sg - 1, a.wg_end) : 0, gs = SK ? nr : AK_PICK(sg, a.wg_end) - wg0;
   const int w = SK ? r : (int)blockIdx.x - wg0;
   const int n = AK_PICK(sg, sgs.n), n_b4 = (n + 3) >> 2;
   // the quads the activation image holds: [q0, q0 + nqs) (SK: stripe psk; else all)
-  const int q0 = SK ? stripe_begin(psk, nquad, P, 2) : 0;
-  const int nqs = SK ? stripe_begin(psk + 1, nquad, P, 2) - q0 : nquad;
+  const int q0 = SK ? 2 * stripe_tile(psk) : 0;
+  const int nqs = SK ? 2 * stripe_tile(psk + 1) - q0 : nquad;
   // 32-bit divisions (w < 1024 workgroups, < 2^21 blocks): a 64-bit one is a long instruction sequence on the GPU
   const int b_lo = (int)((unsigned)w * (unsigned)n_b4 / (unsigned)gs);
   const int nb = (int)((unsigned)(w + 1) * (unsigned)n_b4 / (unsigned)gs) - b_lo;
@@ -223,12 +227,14 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
     for (int i = tid; i < nb; i += 64 * nwv) tickets[i] = 0;
   if (tid < 128) reinterpret_cast<uint32_t*>(lds)[tid] = 0u;
 
-  // ---- activations, step 1: this lane's bf16 inputs, requested and waited for before any weight request (behind
-  // the weight requests of the whole GPU, x would arrive microseconds late)
+  // ---- activations, step 1: this lane's bf16 inputs, requested before any weight request (behind the weight requests
+  // of the whole GPU, x would arrive microseconds late); the set-up below and the first weight requests overlap x's
+  // round trip
   const int gpt = nqs * 4;  // groups per token (of the image)
   const int sub = lane % LPU, units = gpt * MT, ustride = nwv * UPW;
   const int u0 = wave * UPW + lane / LPU;
-  const int npass = (units + ustride - 1) / ustride;
+  const int npass = (units + ustride - 1) >> (lg_nwv + (UPW == 4 ? 2 : 0));
+  static_assert(UPW == 4, "four units per wave");
   uint4 xv[XB];
   // ACT: x is gate_up [mm][2k], the activation SiLU(gate) * up of the two halves (the same value as ak_silu_mul's)
   constexpr bool act = ACT;
@@ -239,11 +245,14 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
   auto xload = [&](int pass0) {
 #pragma unroll
     for (int b = 0; b < XB; ++b) {
-      // lanes past the end load from x[0] (zero-selected); passes past npass load nothing (a wave-uniform branch)
+      // lanes and passes past the end select zeros.  One launch per step: they load from x[0] (cached; unconditional
+      // loads, which the compiler counts exactly, so that it waits for x alone, not for the weights requested after
+      // it).  Chained: passes past the end load nothing (x's loads are device-coherent, the last requests of the
+      // step; thousands of them at one address would queue at the memory side)
       const int u = u0 + (pass0 + b) * ustride, t = MT == 1 ? 0 : u / gpt, gk = (4 * q0 + u - t * gpt) * kG;
       const bool ok = u < units && t < mm && gk < k;
       xv[b] = make_uint4(0u, 0u, 0u, 0u);
-      if (pass0 + b < npass) {
+      if (!CHAIN || pass0 + b < npass) {
         const int xo = ok ? t * xk + gk : 0;  // the unit's group
         if constexpr (CHAIN) {  // device-coherent: x may be an earlier step's output, written by another XCD
           auto ld = [&](int o) {
@@ -271,25 +280,18 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
   };
   // a chained step that depends on earlier steps requests its first weights before it waits for them (below)
   const bool late_x = CHAIN && wait;
-  if (!late_x) {
-    xload(0);
-#pragma unroll
-    for (int b = 0; b < XB; ++b) asm volatile("" ::"v"(xv[b].x), "v"(xv[b].y), "v"(xv[b].z), "v"(xv[b].w));
-  }
+  if (!late_x) xload(0);
 
   // ---- this wave's tasks: stripe set j, tiles [ta, tb), blocks b0w, b0w + bstep, ... < nb
-  const int j = wave % SPLIT, bstep = nwv / SPLIT, b0w = wave / SPLIT;
+  constexpr int LGS = SPLIT == 1 ? 0 : SPLIT == 2 ? 1 : SPLIT == 4 ? 2 : 3;
+  const int j = wave % SPLIT, bstep = nwv >> LGS, b0w = wave / SPLIT;
   const int pa = SK ? psk : j * P / SPLIT, pb = SK ? psk + 1 : (j + 1) * P / SPLIT;
-  const int ta = stripe_begin(pa, nquad, P, 2) >> 1, tb = stripe_begin(pb, nquad, P, 2) >> 1;
-  const int ntw = b0w < nb ? (nb - b0w + bstep - 1) / bstep : 0;
+  const int ta = stripe_tile(pa), tb = stripe_tile(pb);
+  const int ntw = b0w < nb ? (nb - b0w + bstep - 1) >> (lg_nwv - LGS) : 0;
   const int nitems = ntw * (tb - ta);
-  // bit t - ta set when tile t is the last of its stripe (tiles < ta + 128)
-  unsigned long long ends0 = 0, ends1 = 0;
-  for (int p = pa; p < pb; ++p) {
-    const int r = (stripe_begin(p + 1, nquad, P, 2) >> 1) - 1 - ta;
-    if (r < 64) ends0 |= 1ull << r;
-    else ends1 |= 1ull << (r - 64);
-  }
+  // stripe ends: a.ends (bit t: tile t ends a stripe; at most 64 tiles without split-K); a split-K wave has one
+  // stripe, which ends at tile tb - 1
+  const unsigned long long ends = a.ends;
 
   // ---- weight addressing: per lane fixed, per item scalar.  Rows past the segment's end (padding of the last block)
   // read other rows or, past the buffer, zeros; their results are not written.
@@ -401,8 +403,7 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
   for (int t = 0; t < MT; ++t) acc[t] = 0.f, yrun[t] = 0.f;
   // one item without branches: an[] = the accumulators before a stripe end reset them (used only at a stripe end)
   auto core = [&](const TileRaw<BITS>& bf, float (&an)[MT], bool& end, int& eg, int& ep) {
-    const int r0 = ct - ta;
-    end = ((r0 < 64 ? ends0 >> r0 : ends1 >> (r0 - 64)) & 1ull) != 0;
+    end = SK ? ct + 1 == tb : ((ends >> ct) & 1ull) != 0;
     Raw<BITS> rq[2];
     split_tile<BITS>(bf, rq[0], rq[1]);
 #pragma unroll
@@ -603,7 +604,7 @@ int plan_m1d(I8Args& a, int bits, int mt, bool chain, M1dShape& sh) {
   const int ntile = a.nquad / 2;
   for (int i = 0; i < g.nseg; ++i)  // buffer offsets are 32-bit
     if ((long long)ntile * g.n[i] * 128 * bits >= (1ll << 31)) return AK_INVALID;
-  if (x_bytes > 150 * 1024) return AK_INVALID;
+  if (x_bytes > 150 * 1024 || a.nquad / 2 > 64) return AK_INVALID;  // (the stripe-end mask covers 64 tiles)
   int total = 0;
   for (int i = 0; i < g.nseg; ++i) total += (g.n[i] + 3) / 4;
   const int cus = num_cus();
@@ -794,7 +795,7 @@ int i8_gemv_m1(int bits, const void* x, int m, const Segs& g, int k, int group, 
   a.k = k;
   a.nquad = kpad(k) / kG / 4;
   a.qpt = 2;
-  a.P = stripe_count(a.nquad, a.qpt);
+  set_tile_stripes(a);
   a.nb = 0;
   a.part = nullptr;
   a.cnt = nullptr;
@@ -844,7 +845,7 @@ int m1d_chain_make(int nsteps, const int* bits, const void* const* x, const int*
     a.k = k[i];
     a.nquad = kpad(k[i]) / kG / 4;
     a.qpt = 2;
-    a.P = stripe_count(a.nquad, a.qpt);
+    set_tile_stripes(a);
     a.nb = 0;
     a.part = nullptr;
     a.cnt = nullptr;
@@ -915,7 +916,7 @@ int m1d_tune_query(int bits, int m, const Segs& g, int k, int* split, int* nwv, 
   a.k = k;
   a.nquad = kpad(k) / kG / 4;
   a.qpt = 2;
-  a.P = stripe_count(a.nquad, a.qpt);
+  set_tile_stripes(a);
   a.nb = 0;
   a.part = nullptr;
   a.cnt = nullptr;
