@@ -20,7 +20,7 @@ BENCH_LIB = os.path.join(HERE, "libagens_bench.so")
 HOST = os.path.join(HERE, "host")
 HOST_LIB = os.path.join(HERE, "libagens_linear.so")
 SOURCES = ["ak_runtime.hip", "wq_layout.hip", "wq_exact.hip", "wq_i8.hip", "wq_i8m1d.hip", "wq_i8mt.hip", "wq_api.hip",
-           "wq_prefill.hip", "wq_gemm.hip", "i8_gemv.hip", "bf16_gemv_bi.hip", "silu_mul.hip"]
+           "wq_prefill.hip", "wq_gemm.hip", "wq_mm.hip", "i8_gemv.hip", "bf16_gemv_bi.hip", "silu_mul.hip"]
 
 
 def hipcc():

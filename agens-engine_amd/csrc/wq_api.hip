@@ -22,6 +22,7 @@ int exact_ct_gemv(const void* x, const int32_t* packed, const void* scales, void
 int i8_gemv(int bits, const void* x, int m, const Segs& g, int k, int group, hipStream_t s);
 int i8_gemv_m1(int bits, const void* x, int m, const Segs& g, int k, int group, hipStream_t s, int act = 0);
 int i8_gemv_mt(int bits, const void* x, int m, const Segs& g, int k, int group, hipStream_t s, int act = 0);
+int mm_gemv(int bits, const void* x, int m, const Segs& g, int k, int group, hipStream_t s, int act);
 int m1d_chain_make(int nsteps, const int* bits, const void* const* x, const int* m, const int* k, const Segs* segs,
                    const int* wait, const int* act, void** table, int* mt_out, size_t* smem_out);
 int m1d_chain_launch(const void* table, int nsteps, int mt, size_t smem, hipStream_t s);
@@ -43,6 +44,22 @@ bool exact_mode() {
     env = (v && v[0] == '1') ? 1 : 0;
   }
   return env == 1;
+}
+
+// The smallest token count routed to the fp16-MFMA kernel (wq_mm.hip) in the default numerics: the measured crossover
+// with the integer-limb kernels (below it those are faster; see the design notes' crossover table).  0: never (the
+// integer numerics for every m, rows bit-identical for any m); set through ak_wq_set_mm_min or AGENS_WQ_MM_MIN.
+constexpr int kMmMinDefault = 9;
+int g_mm_min = -1;
+
+int mm_min() {
+  if (g_mm_min >= 0) return g_mm_min;
+  static int env = -2;
+  if (env == -2) {
+    const char* v = getenv("AGENS_WQ_MM_MIN");
+    env = v && v[0] ? atoi(v) : -1;
+  }
+  return env >= 0 ? env : kMmMinDefault;
 }
 
 bool group_ok(int k, int group) { return (group == 64 || group == 128) && k % group == 0 && k % 32 == 0; }
@@ -105,6 +122,11 @@ int gemv(int bits, const void* x, int m, int nseg, const void* const* wt, const 
     if (n[i] < 1 || !wt[i] || !st[i] || !y[i] || (ldy && ldy[i] < n[i])) return AK_INVALID;
   const bool exact = bf16w || (!force_default && exact_mode());
   if (act && exact) return AK_INVALID;  // the fused activation is in the default path's kernels only
+  const int mmin = mm_min();
+  if (!exact && mmin > 0 && m >= mmin) {  // above the crossover: the fp16-MFMA kernel, all tokens at once
+    const int e = mm_gemv(bits, x, m, make_segs(nseg, wt, st, y, n, ldy, 16), k, group, s, act);
+    if (e != AK_INVALID) return e;
+  }
   for (int m0 = 0; m0 < m; m0 += kMaxTokensPerLaunch) {
     const int mm = m - m0 < kMaxTokensPerLaunch ? m - m0 : kMaxTokensPerLaunch;
     void* yy[kMaxSegs];
@@ -313,9 +335,12 @@ int ak_wq_chain_create(const ak_wq_step* steps, int nsteps, void** chain) {
     return AK_OOM;
   }
   memcpy(c->steps, steps, sizeof(ak_wq_step) * (size_t)nsteps);
+  // the chained kernel computes the integer numerics: a step that one launch would route to the fp16-MFMA kernel
+  // (m at or above its crossover) makes the chain run one launch per step, so that both give the same bits
   bool chainable = !exact_mode();
+  const int mmin = mm_min();
   for (int i = 0; i < nsteps && chainable; ++i)
-    chainable = steps[i].bf16w == 0 && steps[i].group == 128 && steps[i].m <= 2;
+    chainable = steps[i].bf16w == 0 && steps[i].group == 128 && steps[i].m <= 2 && (mmin <= 0 || steps[i].m < mmin);
   if (chainable) {
     int* ib = static_cast<int*>(malloc(sizeof(int) * 5 * (size_t)nsteps));
     const void** xs = static_cast<const void**>(malloc(sizeof(void*) * (size_t)nsteps));
@@ -384,6 +409,11 @@ int ak_wq_tune_query(int bits, int m, int nseg, const int* n, int k, int* split,
   void* dummy[kMaxSegs] = {};
   const Segs g = make_segs(nseg, dummy, dummy, dummy, n, nullptr, 16);
   return m1d_tune_query(bits, m, g, k, split, nwv, sk);
+}
+
+int ak_wq_set_mm_min(int m) {
+  g_mm_min = m < 0 ? -1 : m;
+  return 0;
 }
 
 int ak_w4_set_mma(int mode) {

@@ -19,6 +19,12 @@ int ak_wq_tune_override(int split, int nwv, int sk);
  * applied): 0 and *split, *nwv, *sk (1: split-K across workgroups), or 1 if the shape is not one this kernel takes. */
 int ak_wq_tune_query(int bits, int m, int nseg, const int* n, int k, int* split, int* nwv, int* sk);
 
+/* The smallest token count (m) that ak_wq_gemv_kt_multi and its conveniences route to the fp16-MFMA kernel in the
+ * default numerics (group 128): m >= this many tokens take it, fewer take the integer-limb kernels.  0: never (the
+ * integer numerics for every m: rows bit-identical for any m); negative: the compiled-in measured crossover (or the
+ * environment variable AGENS_WQ_MM_MIN).  Process-wide.  Always 0. */
+int ak_wq_set_mm_min(int m);
+
 #ifdef __cplusplus
 }
 #endif

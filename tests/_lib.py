@@ -312,6 +312,7 @@ def kernels():
             "ak_wq_chain_destroy": (i, [vp]),
             "ak_wq_chain_status": (i, []),
             "ak_w4_set_mma": (i, [i]),
+            "ak_wq_set_mm_min": (i, [i]),
             "ak_w4_set_lean": (i, [i]),
             "ak_w4_set_tma": (i, [i]),
         }

@@ -31,9 +31,11 @@ def gpu():
     n = ctypes.c_int(0)
     assert K.ak_device_count(ctypes.byref(n)) == 0 and n.value >= 1, "no GPU visible"
     K.ak_w4_set_mma(1)
+    K.ak_wq_set_mm_min(0)  # the integer numerics at every m: the subject of this module
     yield K
     K.ak_w4_set_mma(1)
     K.ak_w4_set_mma(-1)
+    K.ak_wq_set_mm_min(-1)
 
 
 def special_x(m, k, group, seed):
