@@ -8,8 +8,8 @@
 // ones round toward zero in fp16's subnormal range); a stored code n enters as the exact fp16 q = (1024 + n) -
 // (1024 + OFF) (OFF = 8 / 4 / 2): one byte permute (bit pattern 0x6400 | n) and one packed fp16 subtraction per pair
 // of codes, from the int8 codes that make_b produces.  D_g = (chain of k-steps 0, 2) + (chain of k-steps 1, 3), each
-// a chain of 32-input MFMAs from zero (exact products, fp32 accumulation); acc = fmaf(D_g * 2^-s, scale_g, acc) over a stripe's groups in order -- the
-// reference tensor-core kernel's per-group form (w4_gemv.cu:1044-1052: exact q in the MMA, fmaf of the group sum with
+// a chain of 32-input MFMAs from zero (exact products, fp32 accumulation); acc = fmaf(D_g * 2^-s, scale_g, acc) over
+// a stripe's groups in order -- the reference tensor-core kernel's per-group form (w4_gemv.cu:1044-1052: exact q in the MMA, fmaf of the group sum with
 // the scale) -- with stripes as the integer numerics (P = min(8, #tiles) contiguous runs of whole 1024-input tiles),
 // y = stripe partials added left to right, bf16 RNE.  The MFMA computes each output element from its own A row and B
 // column, so a token's outputs do not depend on the other tokens of the launch, and every launch shape (split-K or
@@ -27,10 +27,9 @@
 // Loads and items as the tokens-in-A-rows kernel (wq_i8mt.hip): an item is 16 rows x one quad, whole 128-byte lines
 // per row and load instruction pair, one permlane16 swap per dword pair for W2 / W3.
 //
-// Work decomposition: one persistent workgroup per CU (16 waves) owns a contiguous range of 16-row blocks of one
-// segment; wave w owns NBW blocks per round (blocks w + W (NBW rd + b), W waves: 16 for up to 16 tokens, 8 above)
-// and walks the quads of its k range in order,
-// the NBW blocks of a quad one after the other, with two items in flight.  The activation image covers a chunk of
+// Work decomposition: one persistent workgroup per CU owns a contiguous range of 16-row blocks of one segment; wave w
+// owns NBW blocks per round (blocks w + W (NBW rd + b), W waves: 16 for up to 16 tokens, 8 above) and walks the quads
+// of its k range in order, the NBW blocks of a quad one after the other, with two items in flight.  The activation image covers a chunk of
 // cq quads at a time (all tokens); with more than one chunk the workgroup meets at a barrier, restages, and meets
 // again.  SK (split-K across workgroups, one segment, few rows per CU): workgroup (r, p) computes stripe p of row range
 // r; stripe partials go to scratch with device-coherent stores and the range's last workgroup adds them in stripe
@@ -115,13 +114,6 @@ __device__ __forceinline__ f16x8 mm_b(const i32x4& b0, const i32x4& b1, int j) {
 __device__ __forceinline__ int quad_max(int v) {
   v = max(v, __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false));  // quad_perm [1,0,3,2]
   v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false));  // quad_perm [2,3,0,1]
-  return v;
-}
-
-// quad-wide (4 adjacent lanes) fp32 sum: ((v0 + v1) + (v2 + v3)) in every lane
-__device__ __forceinline__ float quad_sum(float v) {
-  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));  // [1,0,3,2]
-  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));  // [2,3,0,1]
   return v;
 }
 

@@ -1,12 +1,12 @@
 """The MFMA route of ak_wq_gemv_kt_multi (csrc/wq_mm.hip): the default numerics above the measured crossover in m.
 
-Its numerics (codes as subnormal fp16 and power-of-two-scaled fp16 activations in v_mfma_f32_16x16x32_f16, the code
-offset removed through the accumulator start, fp32 accumulation, fmaf of each group sum with its scale) have no bit-for-bit counterpart in the reference (whose tensor-core kernels' bits come from the
-H100 MMA instruction), so parity is against the reference CPU path restated in the oracle: the reference's bound
+Its numerics (exact fp16 q and power-of-two-scaled fp16 activations in v_mfma_f32_16x16x32_f16, fp32 accumulation,
+fmaf of each group sum with its scale) have no bit-for-bit counterpart in the reference (whose tensor-core kernels'
+bits come from the H100 MMA instruction), so parity is against the reference CPU path restated in the oracle: the reference's bound
 |y - ref64| <= 1 bf16 ulp + 1e-5 * sum|x * w| (kernels/bench/test_w4.cu:123-141, with the fp32-accumulation term of
 an MMA route) against fp64, and the north-star tolerance against ora_gemv_ref_f32 (reference.rs:53-71): each output is
-one of the two bf16 neighbours of a value within 2e-3 relative of the fp32 reference.  Size-independent properties at the benchmark shapes: a token's
-outputs do not depend on the other tokens of the launch, on the segments launched with it, or on the token count.
+one of the two bf16 neighbours of a value within 2e-3 relative of the fp32 reference.  Size-independent properties at
+the benchmark shapes: a token's outputs do not depend on the other tokens of the launch, on the segments launched with it, or on the token count.
 """
 import ctypes
 
