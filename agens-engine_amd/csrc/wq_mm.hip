@@ -110,13 +110,6 @@ __device__ __forceinline__ f16x8 mm_b(const i32x4& b0, const i32x4& b1, int j) {
   return r;
 }
 
-// quad-wide (4 adjacent lanes) maximum
-__device__ __forceinline__ int quad_max(int v) {
-  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false));  // quad_perm [1,0,3,2]
-  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false));  // quad_perm [2,3,0,1]
-  return v;
-}
-
 // fp32 of bf16 input i of the 16 dwords X (dword i / 2, low half first)
 __device__ __forceinline__ float x_at(const uint32_t (&X)[16], int i) {
   return __uint_as_float((i & 1) ? (X[i >> 1] & 0xFFFF0000u) : (X[i >> 1] << 16));
@@ -192,13 +185,17 @@ __global__ void __launch_bounds__(mm_waves<NTT>() * 64, 1) mm_kernel(const MmArg
   // them as scaled fp16 in the operand order; the group's scale exponent from its four lanes; padding past k: zeros
   auto stage = [&](int ch) __attribute__((always_inline)) {
     const int q0 = qa + ch * cq, cg = 4 * ((qb - q0 < cq ? qb - q0 : cq));
-    const int units = m * cg * 4, xk = a.act ? 2 * k : k;  // x's token stride
+    // units: per (group g, 16-token block tb) one wave-sized set of 64 lanes, lane = (chunk hh = lane / 16, token
+    // tb * 16 + lane % 16): 16 consecutive lanes write 16 consecutive 16-byte token rows of the image (no LDS bank
+    // conflicts); the group's exponent over its four chunk lanes (16 and 32 lanes apart) by lane exchanges
+    const int ntb = (m + 15) >> 4, units = cg * ntb * 64, xk = a.act ? 2 * k : k;  // x's token stride
     const __amdgpu_buffer_rsrc_t rx =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.x), (short)0, m * xk * 2, kRsrcWord3);
     for (int u = tid; u < units; u += blockDim.x) {
-      const int hh = u & 3, rest = u >> 2, t = rest / cg, g = rest - t * cg;
+      const int hh = (u >> 4) & 3, gi = u >> 6, tb = gi / cg, g = gi - tb * cg, t = tb * 16 + (u & 15);
+      const bool tv = t < m;
       const int i0 = (4 * q0 + g) * kG + 32 * hh;  // first input of the lane chunk
-      const int xo = (t * xk + (i0 < k ? i0 : 0)) * 2;
+      const int xo = ((tv ? t : 0) * xk + (i0 < k ? i0 : 0)) * 2;
       uint32_t X[16];
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
@@ -220,7 +217,10 @@ __global__ void __launch_bounds__(mm_waves<NTT>() * 64, 1) mm_kernel(const MmArg
         const uint32_t w = X[i] & 0x7FFF7FFFu;
         mx = max(mx, max(w & 0xFFFFu, w >> 16));
       }
-      const int e = quad_max((int)mx) >> 7;
+      int mxi = (int)mx;
+      mxi = max(mxi, __shfl_xor(mxi, 16));
+      mxi = max(mxi, __shfl_xor(mxi, 32));
+      const int e = mxi >> 7;
       const int sh = 141 - e < 126 ? 141 - e : 126;  // x * 2^sh: the largest magnitude in [2^14, 2^15)
       uint8_t* dst = img + (size_t)g * gbytes + ((size_t)hh * tl + t) * 16;
       // the scaled inputs in the operand order
@@ -233,9 +233,9 @@ __global__ void __launch_bounds__(mm_waves<NTT>() * 64, 1) mm_kernel(const MmArg
                                                      ldexpf(x_at(X, mm_pos<BITS>(j, 2 * q + 1)), sh));
           __builtin_memcpy(&d[q], &h2, 4);
         }
-        *reinterpret_cast<uint4*>(dst + (size_t)j * 4 * tl * 16) = make_uint4(d[0], d[1], d[2], d[3]);
+        if (tv) *reinterpret_cast<uint4*>(dst + (size_t)j * 4 * tl * 16) = make_uint4(d[0], d[1], d[2], d[3]);
       }
-      if (hh == 0) reinterpret_cast<int*>(meta)[g * tl + t] = -sh;  // D * 2^-s: the group's sum
+      if (tv && hh == 0) reinterpret_cast<int*>(meta)[g * tl + t] = -sh;  // D * 2^-s: the group's sum
     }
   };
 
@@ -321,7 +321,7 @@ __global__ void __launch_bounds__(mm_waves<NTT>() * 64, 1) mm_kernel(const MmArg
     quad_groups<BITS>(bf, rg);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      if (s == 2) asm volatile("" ::: "memory");  // two groups' operands live at a time
+      if (NTT == 1 && s == 2) asm volatile("" ::: "memory");  // one tile: two groups' operands live at a time
       i32x4 b0, b1;
       make_b<BITS>(rg[s], b0, b1);
       constexpr int tlr = TL;
@@ -331,19 +331,25 @@ __global__ void __launch_bounds__(mm_waves<NTT>() * 64, 1) mm_kernel(const MmArg
       const int jst = dz ? 0 : 4 * TL * 16;
       const uint8_t* ab = dz ? lds + lane * 16 : img + (size_t)g * 256 * tlr + ((size_t)h * tlr + a_tok) * 16;
       const int* eb = dz ? reinterpret_cast<const int*>(lds) : reinterpret_cast<const int*>(meta) + g * tlr + m_tok;
+      // the group's B operands once (several tiles reuse them), and with several tiles every A operand of the group
+      // requested before the first MFMA (2 waves per SIMD: the LDS latency is hidden by requests in flight)
+      f16x8 B[4], A[NTT][4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) B[j] = mm_b<BITS>(b0, b1, j);
+#pragma unroll
+      for (int tt = 0; tt < NTT; ++tt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) __builtin_memcpy(&A[tt][j], ab + (size_t)j * jst + tt * 256, 16);
 #pragma unroll
       for (int tt = 0; tt < NTT; ++tt) {
-        if (tt) asm volatile("" ::: "memory");  // one token tile's operands live at a time
         // two independent chains (k-steps 0, 2 and 1, 3), added at the end: half the dependent MFMA latency
         f32x4 d = {0.f, 0.f, 0.f, 0.f}, e = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          f16x8 A;
-          __builtin_memcpy(&A, ab + (size_t)j * jst + tt * 256, 16);
           if (j & 1)
-            e = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, mm_b<BITS>(b0, b1, j), e, 0, 0, 0);
+            e = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[tt][j], B[j], e, 0, 0, 0);
           else
-            d = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, mm_b<BITS>(b0, b1, j), d, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[tt][j], B[j], d, 0, 0, 0);
         }
         d += e;
         const i32x4 xe = *reinterpret_cast<const i32x4*>(eb + 16 * tt);  // -s per token
