@@ -21,6 +21,10 @@ struct I8Args {
   // ends a stripe (up to 64 tiles)
   unsigned pmul = 0;
   unsigned long long ends = 0;
+  // chained launches: a tagged copy of each segment's outputs for the next step (32-bit words bf16 | tag << 16, laid
+  // out as y), and the tagged copy this step's activations are read from (written by the step before it)
+  uint32_t* ytg[4] = {nullptr, nullptr, nullptr, nullptr};
+  const uint32_t* xtg = nullptr;
 };
 
 // The P (<= 8) stripe partials of one output of a split-K launch, at float offsets off + q * stride (q < P) of base,

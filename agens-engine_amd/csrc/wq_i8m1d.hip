@@ -120,6 +120,17 @@ constexpr long long kChainSpinTicks = 20000000;  // 0.2 s of the 100 MHz wall cl
 __device__ __attribute__((aligned(256))) uint32_t g_chain_flags[kChainMaxWg * kChainFlagStride];
 __device__ uint32_t g_chain_err;
 
+// Tagged activations: where a step's x is the output of the step just before it, that step also writes its outputs
+// as 32-bit words (bf16 value | tag << 16, tag = the launch's 16-bit epoch) to a buffer of the chain, and the step
+// reads that buffer instead of waiting at the grid barrier: each wave loads its own activations device-coherently
+// until every word it holds carries the launch's tag.  One write-through and one read round trip then separate the
+// steps, instead of the write acknowledgement, the flag store, the poll and the activation read of the barrier.
+// x complete means every workgroup of the step before has finished it (outputs are written at the end of a step, and
+// every output row is written); the host takes a tagged wait only where that step itself waited for the one before
+// it and the step after this one waits, so that the grid-barrier guarantee (every earlier step complete) still holds
+// wherever a later step relies on it.
+constexpr uint32_t kTagMask = 0xFFFFu;
+
 // Wave 0 polls until the flags of workgroups [0, nwg) are all at least `target` (wrap-safe).  It polls before it
 // requests weights of its own, so that no poll waits behind them.
 __device__ __forceinline__ void chain_poll(uint32_t target) {
@@ -159,14 +170,15 @@ __device__ __forceinline__ void lds_barrier() {
 }
 
 // One GEMV step of one workgroup.  CHAIN: part of a chained launch (workgroups past the step's grid return at once;
-// with `wait`, the step waits for all workgroups to reach `target` after its first weight requests; activations are
-// read and outputs written device-coherently).
+// with `wait`, the step waits for all workgroups to reach `target` after its first weight requests; with a.xtg, it
+// polls its tagged activations for `tag` instead; activations are read and outputs written device-coherently, and
+// the tagged copy of the outputs is written where a.ytg asks for it).
 //
 // SK (split-K across workgroups, one segment): workgroup (r, p) computes stripe p of the rows of range r, converting
 // only that stripe's activations; it writes its stripe partials with device-coherent stores, and the last of the
 // range's P workgroups (device-scope counter) adds them in stripe order and writes y.
 template <int BITS, int SPLIT, int DEPTH, int MT, bool CHAIN, bool SK = false, bool ACT = false>
-__device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wait, uint32_t target) {
+__device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wait, uint32_t target, uint32_t tag) {
   static_assert(!SK || SPLIT == 1, "a split launch gives every wave whole stripes of its blocks");
   constexpr int LPU = kG / 8, UPW = 64 / LPU, XB = 4;
   constexpr int REC = 128 * BITS;  // one row's tile record
@@ -210,6 +222,7 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
   const int b_lo = (int)((unsigned)w * (unsigned)n_b4 / (unsigned)gs);
   const int nb = (int)((unsigned)(w + 1) * (unsigned)n_b4 / (unsigned)gs) - b_lo;
   uint16_t* const yseg = AK_PICK(sg, sgs.y);
+  uint32_t* const ytg = CHAIN ? AK_PICK(sg, a.ytg) : nullptr;
   const int ldy = AK_PICK(sg, sgs.ldy);
 
   // LDS: zeros [512 B] | limbs [MT][nquad][half 2][chunk 16][limb 3][16 B] | meta [MT][nquad][4] int4 |
@@ -242,7 +255,40 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
   const __amdgpu_buffer_rsrc_t rx =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.x), (short)0, mm * xk * 2, kRsrcWord3);
   (void)rx;
-  auto xload = [&](int pass0) {
+  const bool tagged = CHAIN && a.xtg != nullptr;
+  const __amdgpu_buffer_rsrc_t rxt =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(a.xtg), (short)0, mm * xk * 4, kRsrcWord3);
+  (void)rxt;
+  const uint32_t tag2 = (tag & kTagMask) * 0x10001u;
+  // the lane's four input pairs of the group at element offset o from the tagged copy: values in v, and whether every
+  // word carries the tag
+  auto ld_tagged = [&](int o, uint4& v) __attribute__((always_inline)) {
+    typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+    uint32_t lo[4], hi[4];
+    if constexpr (BITS == 4) {
+      const int b = (o + unit_pair_offset<4>(sub, 0)) * 4;
+      const u32x4 d0 = __builtin_amdgcn_raw_buffer_load_b128(rxt, b, 0, kSc1);
+      const u32x4 d1 = __builtin_amdgcn_raw_buffer_load_b128(rxt, b + 16, 0, kSc1);
+      lo[0] = d0[0], hi[0] = d0[1], lo[1] = d0[2], hi[1] = d0[3];
+      lo[2] = d1[0], hi[2] = d1[1], lo[3] = d1[2], hi[3] = d1[3];
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const u32x2 d = __builtin_amdgcn_raw_buffer_load_b64(rxt, (o + unit_pair_offset<BITS>(sub, c)) * 4, 0, kSc1);
+        lo[c] = d[0], hi[c] = d[1];
+      }
+    }
+    bool ok = true;
+    uint32_t w[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      w[c] = __builtin_amdgcn_perm(hi[c], lo[c], 0x05040100u);                   // the two values
+      ok = ok && __builtin_amdgcn_perm(hi[c], lo[c], 0x07060302u) == tag2;     // the two tags
+    }
+    v = make_uint4(w[0], w[1], w[2], w[3]);
+    return ok;
+  };
+  auto xload = [&](int pass0) __attribute__((always_inline)) {
 #pragma unroll
     for (int b = 0; b < XB; ++b) {
       // lanes and passes past the end select zeros.  One launch per step: they load from x[0] (cached; unconditional
@@ -278,8 +324,43 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
       }
     }
   };
+  // a tagged step's activations of pass pass0 + b, reloaded until all of the wave's words carry the launch's tag (a
+  // bounded wait: past it the chain's error flag is raised and the step goes on); one pass at a time, so that only
+  // one pass's tagged words are held in registers
+  auto xpoll = [&](int pass0, int b) __attribute__((always_inline)) {
+    const int u = u0 + (pass0 + b) * ustride, t = MT == 1 ? 0 : u / gpt, gk = (4 * q0 + u - t * gpt) * kG;
+    const bool ok = u < units && t < mm && gk < k;
+    xv[b] = make_uint4(0u, 0u, 0u, 0u);
+    if (pass0 + b >= npass) return;
+    const int xo = ok ? t * xk + gk : 0;
+    const long long t0 = wall_clock64();
+    for (;;) {
+      uint4 g, h2;
+      bool got = ld_tagged(xo, g);
+      if (act) got = ld_tagged(xo + k, h2) && got;
+      if (__all(got || !ok)) {
+        if (act) g = silu_mul8(g, h2);
+        xv[b] = ok ? g : make_uint4(0u, 0u, 0u, 0u);
+        break;
+      }
+      if (wall_clock64() - t0 > kChainSpinTicks) {
+        if ((threadIdx.x & 63) == 0) __hip_atomic_store(&g_chain_err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+  };
+  // the activations of passes pass0 .. pass0 + XB - 1
+  auto xload_wait = [&](int pass0) __attribute__((always_inline)) {
+    if (!tagged) {
+      xload(pass0);
+      return;
+    }
+#pragma unroll
+    for (int b = 0; b < XB; ++b) xpoll(pass0, b);
+  };
   // a chained step that depends on earlier steps requests its first weights before it waits for them (below)
-  const bool late_x = CHAIN && wait;
+  const bool late_x = CHAIN && (wait || tagged);
   if (!late_x) xload(0);
 
   // ---- this wave's tasks: stripe set j, tiles [ta, tb), blocks b0w, b0w + bstep, ... < nb
@@ -343,12 +424,12 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
 
   // ---- the first DEPTH items are requested, then step 2 of the activations: per group the limbs (to LDS), and in
   // meta the bias sums -OFF * sum(d_j) of the three limbs with the activation scale 2^(E - 148) as float bits
-  if (late_x && wave == 0) chain_poll(target);
+  if (wait && late_x && wave == 0) chain_poll(target);
 #pragma unroll
   for (int d = 0; d < DEPTH; ++d) fetch_next(buf[d]);
   if (late_x) {
-    lds_barrier();
-    xload(0);
+    if (wait) lds_barrier();
+    xload_wait(0);
   }
 
   auto convert = [&](int p0) {
@@ -373,7 +454,7 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
   };
   convert(0);
   for (int p0 = XB; p0 < npass; p0 += XB) {
-    xload(p0);
+    xload_wait(p0);
     convert(p0);
   }
   __syncthreads();
@@ -534,9 +615,12 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
   for (int i = tid; i < MT * nb * 4; i += 64 * nwv) {
     const int t = MT == 1 ? 0 : i / (nb * 4), row = b_lo * 4 + i - t * nb * 4;
     if (t < mm && row < n) {
-      if constexpr (CHAIN)
+      if constexpr (CHAIN) {
         __hip_atomic_store(yseg + (size_t)t * ldy + row, yl[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      else
+        if (ytg)
+          __hip_atomic_store(ytg + (size_t)t * ldy + row, (uint32_t)yl[i] | ((tag & kTagMask) << 16), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+      } else
         yseg[(size_t)t * ldy + row] = yl[i];
     }
   }
@@ -545,7 +629,7 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
 template <int BITS, int SPLIT, int DEPTH, int MT, bool SK = false, bool ACT = false>
 __global__ void __launch_bounds__(1024, 1) i8_m1d_kernel(const I8Args a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  m1d_body<BITS, SPLIT, DEPTH, MT, false, SK, ACT>(a, lds, false, 0u);
+  m1d_body<BITS, SPLIT, DEPTH, MT, false, SK, ACT>(a, lds, false, 0u, 0u);
 }
 
 size_t m1d_x_bytes(int nquad, int mt) { return 512 + (size_t)mt * nquad * (kCPQ * 96 + 4 * 16); }
@@ -737,46 +821,59 @@ constexpr int kSplitK = 256, kAct = 512;
 struct ChainStep {
   I8Args a;
   int kind;  // bits * 16 + SPLIT, + kSplitK for a split-K step, + kAct for a split-K step with SiLU(gate) * up
-  int wait;  // 1: the step reads (or overwrites) what earlier steps wrote or read: wait for all of them
+  int wait;    // 1: the step reads (or overwrites) what earlier steps wrote or read: wait for all of them
+  int signal;  // 1: a later step waits at the grid barrier for this one: signal the flags after it
 };
 
+// epochs: one word per workgroup in the chain's memory, the number of launches of this chain so far (every workgroup
+// counts every launch, so they agree); the tag of a launch is the low 16 bits of its epoch + 1, which differ from the
+// tags the previous launch left in the tagged copies and from their initial zeros
 template <int MT>
-__global__ void __launch_bounds__(1024, 1) i8_chain_kernel(const ChainStep* __restrict__ steps, int nsteps) {
+__global__ void __launch_bounds__(1024, 1) i8_chain_kernel(const ChainStep* __restrict__ steps, int nsteps,
+                                                           uint32_t* __restrict__ epochs) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   constexpr int D = m1d_depth(MT);
   uint32_t* const flag = g_chain_flags + blockIdx.x * kChainFlagStride;
-  // every workgroup's flag holds the same count between chained launches (all of them signal every step)
+  // every workgroup's flag holds the same count between chained launches (all of them signal the last step)
   const uint32_t f0 = __builtin_amdgcn_readfirstlane(__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  const uint32_t ep = __builtin_amdgcn_readfirstlane(epochs[blockIdx.x]);
+  const uint32_t tag = (ep + 1u) & kTagMask;
   for (int s = 0; s < nsteps; ++s) {
     const ChainStep st = steps[s];  // a copy: the step's fields live in scalar registers
     const bool w = st.wait != 0;
     const uint32_t target = f0 + (uint32_t)s;
     switch (st.kind) {
-      case 4 * 16 + 1: m1d_body<4, 1, D, MT, true>(st.a, lds, w, target); break;
-      case 4 * 16 + 2: m1d_body<4, 2, D, MT, true>(st.a, lds, w, target); break;
-      case 4 * 16 + 4: m1d_body<4, 4, D, MT, true>(st.a, lds, w, target); break;
-      case 4 * 16 + 8: m1d_body<4, 8, D, MT, true>(st.a, lds, w, target); break;
-      case 3 * 16 + 1: m1d_body<3, 1, D, MT, true>(st.a, lds, w, target); break;
-      case 3 * 16 + 2: m1d_body<3, 2, D, MT, true>(st.a, lds, w, target); break;
-      case 3 * 16 + 4: m1d_body<3, 4, D, MT, true>(st.a, lds, w, target); break;
-      case 3 * 16 + 8: m1d_body<3, 8, D, MT, true>(st.a, lds, w, target); break;
-      case 2 * 16 + 1: m1d_body<2, 1, D, MT, true>(st.a, lds, w, target); break;
-      case 2 * 16 + 2: m1d_body<2, 2, D, MT, true>(st.a, lds, w, target); break;
-      case 2 * 16 + 4: m1d_body<2, 4, D, MT, true>(st.a, lds, w, target); break;
-      case kSplitK + 4 * 16 + 1: m1d_body<4, 1, D, MT, true, true>(st.a, lds, w, target); break;
-      case kSplitK + 3 * 16 + 1: m1d_body<3, 1, D, MT, true, true>(st.a, lds, w, target); break;
-      case kSplitK + 2 * 16 + 1: m1d_body<2, 1, D, MT, true, true>(st.a, lds, w, target); break;
-      case kAct + kSplitK + 4 * 16 + 1: m1d_body<4, 1, D, MT, true, true, true>(st.a, lds, w, target); break;
-      case kAct + kSplitK + 3 * 16 + 1: m1d_body<3, 1, D, MT, true, true, true>(st.a, lds, w, target); break;
-      case kAct + kSplitK + 2 * 16 + 1: m1d_body<2, 1, D, MT, true, true, true>(st.a, lds, w, target); break;
-      default: m1d_body<2, 8, D, MT, true>(st.a, lds, w, target); break;
+      case 4 * 16 + 1: m1d_body<4, 1, D, MT, true>(st.a, lds, w, target, tag); break;
+      case 4 * 16 + 2: m1d_body<4, 2, D, MT, true>(st.a, lds, w, target, tag); break;
+      case 4 * 16 + 4: m1d_body<4, 4, D, MT, true>(st.a, lds, w, target, tag); break;
+      case 4 * 16 + 8: m1d_body<4, 8, D, MT, true>(st.a, lds, w, target, tag); break;
+      case 3 * 16 + 1: m1d_body<3, 1, D, MT, true>(st.a, lds, w, target, tag); break;
+      case 3 * 16 + 2: m1d_body<3, 2, D, MT, true>(st.a, lds, w, target, tag); break;
+      case 3 * 16 + 4: m1d_body<3, 4, D, MT, true>(st.a, lds, w, target, tag); break;
+      case 3 * 16 + 8: m1d_body<3, 8, D, MT, true>(st.a, lds, w, target, tag); break;
+      case 2 * 16 + 1: m1d_body<2, 1, D, MT, true>(st.a, lds, w, target, tag); break;
+      case 2 * 16 + 2: m1d_body<2, 2, D, MT, true>(st.a, lds, w, target, tag); break;
+      case 2 * 16 + 4: m1d_body<2, 4, D, MT, true>(st.a, lds, w, target, tag); break;
+      case kSplitK + 4 * 16 + 1: m1d_body<4, 1, D, MT, true, true>(st.a, lds, w, target, tag); break;
+      case kSplitK + 3 * 16 + 1: m1d_body<3, 1, D, MT, true, true>(st.a, lds, w, target, tag); break;
+      case kSplitK + 2 * 16 + 1: m1d_body<2, 1, D, MT, true, true>(st.a, lds, w, target, tag); break;
+      case kAct + kSplitK + 4 * 16 + 1: m1d_body<4, 1, D, MT, true, true, true>(st.a, lds, w, target, tag); break;
+      case kAct + kSplitK + 3 * 16 + 1: m1d_body<3, 1, D, MT, true, true, true>(st.a, lds, w, target, tag); break;
+      case kAct + kSplitK + 2 * 16 + 1: m1d_body<2, 1, D, MT, true, true, true>(st.a, lds, w, target, tag); break;
+      default: m1d_body<2, 8, D, MT, true>(st.a, lds, w, target, tag); break;
     }
     // signal: this workgroup's outputs of steps <= s are stored (each wave waits for its own stores' acknowledgement,
-    // which for sc1 stores means written through to device scope)
-    __builtin_amdgcn_s_waitcnt(kVmcnt0);
-    __syncthreads();
-    if (threadIdx.x == 0) __hip_atomic_store(flag, f0 + (uint32_t)s + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // which for sc1 stores means written through to device scope).  Without a signal the workgroup goes on at once
+    // (its stores complete in the background; the next step's LDS is reused only after the barrier).
+    if (st.signal || s + 1 == nsteps) {
+      __builtin_amdgcn_s_waitcnt(kVmcnt0);
+      __syncthreads();
+      if (threadIdx.x == 0) __hip_atomic_store(flag, f0 + (uint32_t)s + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+      lds_barrier();
+    }
   }
+  if (threadIdx.x == 0) epochs[blockIdx.x] = ep + 1u;
 }
 
 }  // namespace
@@ -833,10 +930,30 @@ int m1d_chain_make(int nsteps, const int* bits, const void* const* x, const int*
   ChainStep* h = static_cast<ChainStep*>(calloc((size_t)nsteps, sizeof(ChainStep)));
   if (!h) return AK_OOM;
   size_t smem = 0;
-  // the table, then the split-K steps' scratch (counters and partials, zeroed)
+  // the table, then (zeroed) the workgroups' epochs, the tagged output copies and the split-K steps' scratch (counters
+  // and partials)
   const size_t table_bytes = ((size_t)nsteps * sizeof(ChainStep) + 255) & ~(size_t)255;
-  size_t total = table_bytes;
+  size_t total = table_bytes + kChainMaxWg * 4;
   std::vector<size_t> zoff((size_t)nsteps, 0);
+  // tagged waits: step i reads its activations from a tagged copy of segment tseg[i] of step i - 1's outputs where
+  // that segment holds all of them (x is its start, its rows dense, m * k of x within its m * n outputs), step i - 1
+  // waited for the step before it (or is the first) and step i + 1 waits (or there is none); AK_CHAIN_TAGS=0: never
+  std::vector<int> tseg((size_t)nsteps, -1);
+  std::vector<size_t> toff((size_t)nsteps, 0);
+  const char* ev = getenv("AK_CHAIN_TAGS");
+  const bool tags_on = !(ev && atoi(ev) == 0);
+  for (int i = 1; i < nsteps && tags_on; ++i) {
+    if (!wait[i] || (i > 1 && !wait[i - 1]) || (i + 1 < nsteps && !wait[i + 1])) continue;
+    const Segs& p = segs[i - 1];
+    const long long need = (long long)m[i] * k[i] * (act[i] ? 2 : 1);
+    for (int j = 0; j < p.nseg; ++j)
+      if (p.y[j] == x[i] && p.ldy[j] == p.n[j] && need <= (long long)m[i - 1] * p.n[j]) {
+        tseg[(size_t)i] = j;
+        toff[(size_t)i] = total;
+        total += ((size_t)m[i - 1] * p.n[j] * 4 + 255) & ~(size_t)255;
+        break;
+      }
+  }
   for (int i = 0; i < nsteps; ++i) {
     I8Args& a = h[i].a;
     a.segs = segs[i];
@@ -849,7 +966,8 @@ int m1d_chain_make(int nsteps, const int* bits, const void* const* x, const int*
     a.nb = 0;
     a.part = nullptr;
     a.cnt = nullptr;
-    h[i].wait = i > 0 && wait[i] ? 1 : 0;
+    h[i].wait = i > 0 && wait[i] && tseg[(size_t)i] < 0 ? 1 : 0;
+    h[i].signal = i + 1 < nsteps && wait[i + 1] && tseg[(size_t)i + 1] < 0 ? 1 : 0;
     a.act = act[i];
     int nr = 0;
     size_t sks = 0, zb = 0;
@@ -872,11 +990,17 @@ int m1d_chain_make(int nsteps, const int* bits, const void* const* x, const int*
   void* d = nullptr;
   int e = (int)hipMalloc(&d, total);
   if (!e && total > table_bytes) e = (int)hipMemset(static_cast<uint8_t*>(d) + table_bytes, 0, total - table_bytes);
-  for (int i = 0; i < nsteps && !e; ++i)
+  for (int i = 0; i < nsteps && !e; ++i) {
+    if (tseg[(size_t)i] >= 0) {
+      uint32_t* tb = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(d) + toff[(size_t)i]);
+      h[i].a.xtg = tb;
+      h[i - 1].a.ytg[tseg[(size_t)i]] = tb;
+    }
     if (zoff[(size_t)i]) {
       h[i].a.cnt = reinterpret_cast<int*>(static_cast<uint8_t*>(d) + zoff[(size_t)i]);
       h[i].a.part = reinterpret_cast<float*>(static_cast<uint8_t*>(d) + zoff[(size_t)i] + 4096);
     }
+  }
   if (!e) e = (int)hipMemcpy(d, h, (size_t)nsteps * sizeof(ChainStep), hipMemcpyHostToDevice);
   free(h);
   if (e) {
@@ -891,10 +1015,12 @@ int m1d_chain_make(int nsteps, const int* bits, const void* const* x, const int*
 
 int m1d_chain_launch(const void* table, int nsteps, int mt, size_t smem, hipStream_t s) {
   const ChainStep* t = static_cast<const ChainStep*>(table);
+  uint32_t* ep = reinterpret_cast<uint32_t*>(const_cast<uint8_t*>(static_cast<const uint8_t*>(table)) +
+                                             (((size_t)nsteps * sizeof(ChainStep) + 255) & ~(size_t)255));
   if (mt == 1)
-    hipLaunchKernelGGL(i8_chain_kernel<1>, dim3(num_cus()), dim3(1024), smem, s, t, nsteps);
+    hipLaunchKernelGGL(i8_chain_kernel<1>, dim3(num_cus()), dim3(1024), smem, s, t, nsteps, ep);
   else
-    hipLaunchKernelGGL(i8_chain_kernel<2>, dim3(num_cus()), dim3(1024), smem, s, t, nsteps);
+    hipLaunchKernelGGL(i8_chain_kernel<2>, dim3(num_cus()), dim3(1024), smem, s, t, nsteps, ep);
   return (int)hipGetLastError();
 }
 

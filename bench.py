@@ -116,7 +116,11 @@ class QLinear:
             cs = ctx.alloc(n * k // group * 2, keep=False)
         lo, span = code_range(bits)
         ctx.check(B.agb_gen_container(seed, n, k, lo, span, ct, None), "gen container")
-        ctx.check(B.agb_gen_scales(seed + 1, n * k // group, 0.02, 1e-4, cs, None), "gen scales")
+        # scales |N(0,1)| / sqrt(k E[q^2]) (E[q^2] of uniform codes): outputs stay about unit size through the sweep's
+        # data flow, each step reading the one before it
+        eq2 = {4: 21.5, 3: 5.5, 2: 1.5}[bits]
+        ctx.check(B.agb_gen_scales(seed + 1, n * k // group, float(1.0 / np.sqrt(k * eq2)), 1e-6, cs, None),
+                  "gen scales")
         ctx.check(K.ak_wq_repack_kt(bits, ct, cs, self.wt, self.st, n, k, group, None), "repack")
         self.container = None
         if keep_container:  # host copy of the container for the CPU baseline
@@ -160,7 +164,10 @@ def layer_bits(layer):
 def build_sweep(ctx, m, cpu_layers, tp=1):
     """64 layers + LM head; returns (plan, meta, containers for the CPU baseline).  tp > 1: one rank's shard of a
     tensor-parallel layer (m1.rs:58-77 tp_rule): q/k/v, gate_up and the LM head by output rows (n / tp), o and down by
-    k (k / tp; the all-reduce of their outputs is not part of this one-GPU build)."""
+    k (k / tp; the all-reduce of their outputs is not part of this one-GPU build).  Each linear reads the output of
+    the one before it, as in a decode step: qkv (layer 0: h; later: the previous layer's down) -> o (x = q) -> gate_up
+    (x = o) -> down (x = the first k rows of gate_up) -> ..., LM head (x = the last down); the attention, norms and
+    residual adds between them are not part of the GEMV path."""
     H, KV, INTER, VOCAB = 5120, 1024, 27648, 152064
     T = tp
     B = ctx.B
@@ -168,13 +175,12 @@ def build_sweep(ctx, m, cpu_layers, tp=1):
     ct = ctx.alloc(VOCAB * H // 2, keep=False)
     cs = ctx.alloc(VOCAB * H // 128 * 2, keep=False)
     xh = ctx.alloc(m * H * 2)
-    xd = ctx.alloc(m * INTER * 2)
     ctx.check(B.agb_gen_x(SEED + 1, m * H, 1.0, xh, None), "gen x")
-    ctx.check(B.agb_gen_x(SEED + 2, m * INTER, 1.0, xd, None), "gen x")
     yq, yk, yv = ctx.alloc(m * H * 2), ctx.alloc(m * KV * 2), ctx.alloc(m * KV * 2)
     yo, yg, ydn = ctx.alloc(m * H * 2), ctx.alloc(m * 2 * INTER * 2), ctx.alloc(m * H * 2)
     ylm = ctx.alloc(m * VOCAB * 2)
     plan, meta, cpu = [], [], []
+    xl = xh  # the layer's input
     for l in range(64):
         b = layer_bits(l)
         s = SEED * 1000 + 10 * l
@@ -185,13 +191,14 @@ def build_sweep(ctx, m, cpu_layers, tp=1):
         o = QLinear(ctx, s + 6, H, H // T, b, ct=ct, cs=cs, keep_container=keep)
         gu = QLinear(ctx, s + 8, 2 * INTER // T, H, b, ct=ct, cs=cs, keep_container=keep)
         dn = QLinear(ctx, s + 10, H, INTER // T, b, ct=ct, cs=cs, keep_container=keep)
-        plan += [launch(b, m, H, xh, [q, kk, v], [yq, yk, yv]), launch(b, m, H // T, xh, [o], [yo]),
-                 launch(b, m, H, xh, [gu], [yg]), launch(b, m, INTER // T, xd, [dn], [ydn])]
+        plan += [launch(b, m, H, xl, [q, kk, v], [yq, yk, yv]), launch(b, m, H // T, yq, [o], [yo]),
+                 launch(b, m, H, yo, [gu], [yg]), launch(b, m, INTER // T, yg, [dn], [ydn])]
         meta += [("qkv", b), ("o", b), ("gate_up", b), ("down", b)]
         if keep:
-            cpu += [(xh, H, [q, kk, v]), (xh, H // T, [o]), (xh, H, [gu]), (xd, INTER // T, [dn])]
+            cpu += [(xl, H, [q, kk, v]), (yq, H // T, [o]), (yo, H, [gu]), (yg, INTER // T, [dn])]
+        xl = ydn
     lm = QLinear(ctx, SEED * 1000 + 999, VOCAB // T, H, 4, ct=ct, cs=cs)
-    plan.append(launch(4, m, H, xh, [lm], [ylm]))
+    plan.append(launch(4, m, H, ydn, [lm], [ylm]))
     meta.append(("lm_head", 4))
     ctx.check(ctx.K.ak_synchronize(), "sync")
     ctx.free(ct)
@@ -325,7 +332,8 @@ def run_sweep(args, K, B):
         "ms_per_step": round(ms.value, 4), "us_per_sweep": round(ms.value * 1e3, 1),
         "pct_of_peak": round(100 * gbs / HBM_PEAK_GBS, 2), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "int8 MFMA (exact int32 group sums) + fp32 accumulate; bf16 in/out",
-        "data": "synthetic (device-generated int4 container, repacked by ak_wq_repack_kt; random codes/scales/x)",
+        "data": "synthetic (device-generated int4 container, repacked by ak_wq_repack_kt; random codes/scales; "
+                "each linear reads the previous one's output)",
         "config": {"workload": "64-layer 32B decode GEMV sweep: QKV 5120->7168 (q/k/v segments), O 5120->5120, "
                                "gate_up 5120->55296, down 27648->5120, mixed W2/W3/W4 g128 per layer, "
                                "+ W4 LM head 5120->152064",

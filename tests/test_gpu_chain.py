@@ -8,6 +8,7 @@ Bar: bit-identical to the oracle's default numerics applied step by step, and to
 step.
 """
 import ctypes
+import os
 
 import numpy as np
 import pytest
@@ -292,3 +293,60 @@ def test_chain_at_tp8_rank_shapes_matches_oracle(m):
         gemv(lins[0].bits, xin.p, m, [l.L for l in lins], k, 128, ys=ys)
     check(K.ak_synchronize(), "sync")
     assert_same(read_outputs(m, flow), want, "launches vs oracle")
+
+
+def _run_mixed_chain(m, reps, tags):
+    """A: x -> y1; B: y1 -> y2 and C: y2 -> y3 (each reads the step just before it: tagged activations); D: y1 -> y4
+    (reads A's output, three steps back: a grid-barrier wait, so C signals the flags); E: SiLU(gate) * up of y4 -> y5
+    (reads D's output, fused activation: tagged, k split across workgroups).  Returns every run's outputs."""
+    K = kernels()
+    k, inter = 2048, 16384
+    a, b, c = Lin(41, 4096, k, 3), Lin(43, 2048, 4096, 2), Lin(45, 3072, 2048, 4)
+    d, e = Lin(47, 2 * inter, 4096, 3), Lin(49, 1024, inter, 2)
+    x = Dev(m * k * 2)
+    ys = [Dev(m * n * 2) for n in (4096, 2048, 3072, 2 * inter, 1024)]
+    steps = [wq_step(3, x, m, [a.L], [ys[0]], k), wq_step(2, ys[0], m, [b.L], [ys[1]], 4096),
+             wq_step(4, ys[1], m, [c.L], [ys[2]], 2048), wq_step(3, ys[0], m, [d.L], [ys[3]], 4096),
+             wq_step(2, ys[3], m, [e.L], [ys[4]], inter, act=1)]
+    old = os.environ.get("AK_CHAIN_TAGS")
+    os.environ["AK_CHAIN_TAGS"] = "1" if tags else "0"
+    try:
+        ch = Chain(steps)
+    finally:
+        if old is None:
+            del os.environ["AK_CHAIN_TAGS"]
+        else:
+            os.environ["AK_CHAIN_TAGS"] = old
+    assert ch.chained
+    runs = []
+    for rep in range(reps):
+        xh = gen_x(700 + rep, m * k)
+        check(K.ak_memcpy_h2d(x.p, xh.ctypes.data, xh.nbytes), "h2d")
+        for y in ys:  # outputs the chain does not write would show
+            z = np.zeros(y.nbytes, np.uint8)
+            check(K.ak_memcpy_h2d(y.p, z.ctypes.data, y.nbytes), "zero")
+        ch.run()
+        check(K.ak_synchronize(), "sync")
+        assert K.ak_wq_chain_status() == 0
+        got = [y.get(np.uint16, m * n) for y, n in zip(ys, (4096, 2048, 3072, 2 * inter, 1024))]
+        # the same steps one launch each
+        for lin, xin, kk, y in ((a, x, k, ys[0]), (b, ys[0], 4096, ys[1]), (c, ys[1], 2048, ys[2]),
+                                (d, ys[0], 4096, ys[3])):
+            gemv(lin.bits, xin.p, m, [lin.L], kk, 128, ys=[y])
+        check(K.ak_wq_gemv_kt_silu(2, ys[3].p, m, e.L.wt.p, e.L.st.p, ys[4].p, 1024, 0, inter, 128, None), "silu")
+        check(K.ak_synchronize(), "sync")
+        for si, (g, y, n) in enumerate(zip(got, ys, (4096, 2048, 3072, 2 * inter, 1024))):
+            assert np.array_equal(g, y.get(np.uint16, m * n)), f"m={m} run {rep} step {'ABCDE'[si]}"
+        runs.append(got)
+    return runs
+
+
+@pytest.mark.parametrize("m", [1, 2])
+def test_chain_tagged_and_barrier_waits_mix(m):
+    """Tagged activation waits beside grid-barrier waits in one chain, on three runs in a row with new inputs (the
+    launch tag advances; a stale tag of the run before would read old activations): every step equals one launch per
+    step, and the chain without tagged waits (AK_CHAIN_TAGS=0) gives the same bits."""
+    tagged = _run_mixed_chain(m, 3, True)
+    plain = _run_mixed_chain(m, 1, False)
+    for si, (g, w) in enumerate(zip(tagged[0], plain[0])):
+        assert np.array_equal(g, w), f"step {'ABCDE'[si]}: tagged and barrier-only chains differ"
