@@ -131,6 +131,19 @@ __device__ uint32_t g_chain_err;
 // wherever a later step relies on it.
 constexpr uint32_t kTagMask = 0xFFFFu;
 
+// AK_CHAIN_PROBE builds only (a measurement build, not the library): per step and workgroup, the wall-clock times of
+// the step's start, its activations ready, converted, the item loop done, the outputs issued and the step's end
+#ifdef AK_CHAIN_PROBE
+__device__ unsigned long long g_probe[1024 * 256 * 6];
+__device__ __forceinline__ void probe_mark(uint32_t target, int i) {
+  if (threadIdx.x == 0 && blockIdx.x < 256) g_probe[((target & 1023u) * 256 + blockIdx.x) * 6 + i] = wall_clock64();
+}
+#define AK_PROBE(i) \
+  if constexpr (CHAIN) probe_mark(target, i)
+#else
+#define AK_PROBE(i)
+#endif
+
 // Wave 0 polls until the flags of workgroups [0, nwg) are all at least `target` (wrap-safe).  It polls before it
 // requests weights of its own, so that no poll waits behind them.
 __device__ __forceinline__ void chain_poll(uint32_t target) {
@@ -327,17 +340,36 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
   // a tagged step's activations of pass pass0 + b, reloaded until all of the wave's words carry the launch's tag (a
   // bounded wait: past it the chain's error flag is raised and the step goes on); one pass at a time, so that only
   // one pass's tagged words are held in registers
-  auto xpoll = [&](int pass0, int b) __attribute__((always_inline)) {
+  // (pre: the first attempt's words were requested by xpre, before the step's first weights: a step's last workgroup
+  // to start is the one the step waits for, and its activations must not return behind its own weight requests)
+  uint4 pre_g = make_uint4(0u, 0u, 0u, 0u), pre_h = pre_g;
+  bool pre_got = false;
+  auto xpre = [&]() __attribute__((always_inline)) {
+    const int t = MT == 1 ? 0 : u0 / gpt, gk = (4 * q0 + u0 - t * gpt) * kG;
+    const bool ok = u0 < units && t < mm && gk < k;
+    if (wave * UPW < units) {
+      pre_got = ld_tagged(ok ? t * xk + gk : 0, pre_g);
+      if (act) pre_got = ld_tagged((ok ? t * xk + gk : 0) + k, pre_h) && pre_got;
+    }
+  };
+  auto xpoll = [&](int pass0, int b, bool pre) __attribute__((always_inline)) {
     const int u = u0 + (pass0 + b) * ustride, t = MT == 1 ? 0 : u / gpt, gk = (4 * q0 + u - t * gpt) * kG;
     const bool ok = u < units && t < mm && gk < k;
     xv[b] = make_uint4(0u, 0u, 0u, 0u);
     if (pass0 + b >= npass) return;
     const int xo = ok ? t * xk + gk : 0;
     const long long t0 = wall_clock64();
+    bool first = pre;
     for (;;) {
       uint4 g, h2;
-      bool got = ld_tagged(xo, g);
-      if (act) got = ld_tagged(xo + k, h2) && got;
+      bool got;
+      if (first) {
+        g = pre_g, h2 = pre_h, got = pre_got;
+        first = false;
+      } else {
+        got = ld_tagged(xo, g);
+        if (act) got = ld_tagged(xo + k, h2) && got;
+      }
       if (__all(got || !ok)) {
         if (act) g = silu_mul8(g, h2);
         xv[b] = ok ? g : make_uint4(0u, 0u, 0u, 0u);
@@ -350,14 +382,14 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
       __builtin_amdgcn_s_sleep(1);
     }
   };
-  // the activations of passes pass0 .. pass0 + XB - 1
-  auto xload_wait = [&](int pass0) __attribute__((always_inline)) {
+  // the activations of passes pass0 .. pass0 + XB - 1 (pre: pass 0, requested by xpre)
+  auto xload_wait = [&](int pass0, bool pre) __attribute__((always_inline)) {
     if (!tagged) {
       xload(pass0);
       return;
     }
 #pragma unroll
-    for (int b = 0; b < XB; ++b) xpoll(pass0, b);
+    for (int b = 0; b < XB; ++b) xpoll(pass0, b, pre && b == 0);
   };
   // a chained step that depends on earlier steps requests its first weights before it waits for them (below)
   const bool late_x = CHAIN && (wait || tagged);
@@ -425,11 +457,13 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
   // ---- the first DEPTH items are requested, then step 2 of the activations: per group the limbs (to LDS), and in
   // meta the bias sums -OFF * sum(d_j) of the three limbs with the activation scale 2^(E - 148) as float bits
   if (wait && late_x && wave == 0) chain_poll(target);
+  if (tagged) xpre();
 #pragma unroll
   for (int d = 0; d < DEPTH; ++d) fetch_next(buf[d]);
   if (late_x) {
     if (wait) lds_barrier();
-    xload_wait(0);
+    xload_wait(0, tagged);
+    AK_PROBE(1);
   }
 
   auto convert = [&](int p0) {
@@ -454,10 +488,11 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
   };
   convert(0);
   for (int p0 = XB; p0 < npass; p0 += XB) {
-    xload_wait(p0);
+    xload_wait(p0, false);
     convert(p0);
   }
   __syncthreads();
+  AK_PROBE(2);
 
   // A role: group c >> 2, limb c & 3 (limb 3 reads zeros), chunk 4 * (c >> 2) + h of the quad; half 1 is kCPQ * 48
   // bytes further
@@ -593,6 +628,7 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
     }
   }
   __syncthreads();
+  AK_PROBE(3);
   if constexpr (SK) {
     // every wave's partial stores are acknowledged at device scope before the range's counter moves
     __builtin_amdgcn_s_waitcnt(kVmcnt0);
@@ -604,7 +640,10 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
       if (old == P - 1) __hip_atomic_store(a.cnt + r, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next launch
     }
     __syncthreads();
-    if (!*last) return;
+    if (!*last) {
+      AK_PROBE(4);
+      return;
+    }
     for (int i = tid; i < MT * nb * 4; i += 64 * nwv) {
       const int t = MT == 1 ? 0 : i / (nb * 4), o = i - t * nb * 4;
       const size_t off = ((size_t)t * n_b4 + b_lo) * 4 + o;
@@ -624,6 +663,7 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
         yseg[(size_t)t * ldy + row] = yl[i];
     }
   }
+  AK_PROBE(4);
 }
 
 template <int BITS, int SPLIT, int DEPTH, int MT, bool SK = false, bool ACT = false>
@@ -842,6 +882,9 @@ __global__ void __launch_bounds__(1024, 1) i8_chain_kernel(const ChainStep* __re
     const ChainStep st = steps[s];  // a copy: the step's fields live in scalar registers
     const bool w = st.wait != 0;
     const uint32_t target = f0 + (uint32_t)s;
+#ifdef AK_CHAIN_PROBE
+    probe_mark(target, 0);
+#endif
     switch (st.kind) {
       case 4 * 16 + 1: m1d_body<4, 1, D, MT, true>(st.a, lds, w, target, tag); break;
       case 4 * 16 + 2: m1d_body<4, 2, D, MT, true>(st.a, lds, w, target, tag); break;
@@ -872,6 +915,9 @@ __global__ void __launch_bounds__(1024, 1) i8_chain_kernel(const ChainStep* __re
     } else {
       lds_barrier();
     }
+#ifdef AK_CHAIN_PROBE
+    probe_mark(target, 5);
+#endif
   }
   if (threadIdx.x == 0) epochs[blockIdx.x] = ep + 1u;
 }
@@ -1057,6 +1103,15 @@ int m1d_tune_query(int bits, int m, const Segs& g, int k, int* split, int* nwv, 
   *split = sh.split, *nwv = sh.nwv, *sk = 0;
   return 0;
 }
+
+#ifdef AK_CHAIN_PROBE
+// the probe records and workgroup 0's flag word (a measurement build only)
+extern "C" int ak_chain_probe_read(void* host, size_t bytes, uint32_t* flag0) {
+  int e = (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_probe), bytes, 0, hipMemcpyDeviceToHost);
+  if (!e) e = (int)hipMemcpyFromSymbol(flag0, HIP_SYMBOL(g_chain_flags), 4, 0, hipMemcpyDeviceToHost);
+  return e;
+}
+#endif
 
 // reads and clears the flag a chained launch raises when a wait ran out (0.2 s): 1 if one did since the last call
 int m1d_chain_error(int* err) {
