@@ -130,6 +130,10 @@ __device__ uint32_t g_chain_err;
 // it and the step after this one waits, so that the grid-barrier guarantee (every earlier step complete) still holds
 // wherever a later step relies on it.
 constexpr uint32_t kTagMask = 0xFFFFu;
+// the first read of a step's tagged activations goes through the L2 (1) or device-coherently (0)
+#ifndef AK_TAG_CACHED_FIRST
+#define AK_TAG_CACHED_FIRST 1
+#endif
 
 // AK_CHAIN_PROBE builds only (a measurement build, not the library): per step and workgroup, the wall-clock times of
 // the step's start, its activations ready, converted, the item loop done, the outputs issued and the step's end
@@ -140,6 +144,15 @@ __device__ __forceinline__ void probe_mark(uint32_t target, int i) {
 }
 #define AK_PROBE(i) \
   if constexpr (CHAIN) probe_mark(target, i)
+// per wave: the time its activations were ready and the polls it took
+__device__ unsigned long long g_probe_w[1024 * 256 * 16 * 2];
+__device__ __forceinline__ void probe_wave(uint32_t target, int polls) {
+  if ((threadIdx.x & 63) == 0 && blockIdx.x < 256) {
+    const size_t o = (((target & 1023u) * 256 + blockIdx.x) * 16 + (threadIdx.x >> 6)) * 2;
+    g_probe_w[o] = wall_clock64();
+    g_probe_w[o + 1] = (unsigned long long)polls;
+  }
+}
 #else
 #define AK_PROBE(i)
 #endif
@@ -274,20 +287,25 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
   (void)rxt;
   const uint32_t tag2 = (tag & kTagMask) * 0x10001u;
   // the lane's four input pairs of the group at element offset o from the tagged copy: values in v, and whether every
-  // word carries the tag
-  auto ld_tagged = [&](int o, uint4& v) __attribute__((always_inline)) {
+  // word carries the tag.  cached: read through the L2 (the XCD's workgroups share one request to the memory side; a
+  // stale line there fails the tag check, and the retries read device-coherently)
+  auto ld_tagged = [&](int o, uint4& v, bool cached) __attribute__((always_inline)) {
     typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
     uint32_t lo[4], hi[4];
     if constexpr (BITS == 4) {
       const int b = (o + unit_pair_offset<4>(sub, 0)) * 4;
-      const u32x4 d0 = __builtin_amdgcn_raw_buffer_load_b128(rxt, b, 0, kSc1);
-      const u32x4 d1 = __builtin_amdgcn_raw_buffer_load_b128(rxt, b + 16, 0, kSc1);
+      const u32x4 d0 = cached ? __builtin_amdgcn_raw_buffer_load_b128(rxt, b, 0, 0)
+                              : __builtin_amdgcn_raw_buffer_load_b128(rxt, b, 0, kSc1);
+      const u32x4 d1 = cached ? __builtin_amdgcn_raw_buffer_load_b128(rxt, b + 16, 0, 0)
+                              : __builtin_amdgcn_raw_buffer_load_b128(rxt, b + 16, 0, kSc1);
       lo[0] = d0[0], hi[0] = d0[1], lo[1] = d0[2], hi[1] = d0[3];
       lo[2] = d1[0], hi[2] = d1[1], lo[3] = d1[2], hi[3] = d1[3];
     } else {
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        const u32x2 d = __builtin_amdgcn_raw_buffer_load_b64(rxt, (o + unit_pair_offset<BITS>(sub, c)) * 4, 0, kSc1);
+        const int ob = (o + unit_pair_offset<BITS>(sub, c)) * 4;
+        const u32x2 d = cached ? __builtin_amdgcn_raw_buffer_load_b64(rxt, ob, 0, 0)
+                               : __builtin_amdgcn_raw_buffer_load_b64(rxt, ob, 0, kSc1);
         lo[c] = d[0], hi[c] = d[1];
       }
     }
@@ -348,8 +366,8 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
     const int t = MT == 1 ? 0 : u0 / gpt, gk = (4 * q0 + u0 - t * gpt) * kG;
     const bool ok = u0 < units && t < mm && gk < k;
     if (wave * UPW < units) {
-      pre_got = ld_tagged(ok ? t * xk + gk : 0, pre_g);
-      if (act) pre_got = ld_tagged((ok ? t * xk + gk : 0) + k, pre_h) && pre_got;
+      pre_got = ld_tagged(ok ? t * xk + gk : 0, pre_g, AK_TAG_CACHED_FIRST);
+      if (act) pre_got = ld_tagged((ok ? t * xk + gk : 0) + k, pre_h, AK_TAG_CACHED_FIRST) && pre_got;
     }
   };
   auto xpoll = [&](int pass0, int b, bool pre) __attribute__((always_inline)) {
@@ -360,17 +378,26 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
     const int xo = ok ? t * xk + gk : 0;
     const long long t0 = wall_clock64();
     bool first = pre;
+#ifdef AK_CHAIN_PROBE
+    int polls = 0;
+#endif
     for (;;) {
+#ifdef AK_CHAIN_PROBE
+      ++polls;
+#endif
       uint4 g, h2;
       bool got;
       if (first) {
         g = pre_g, h2 = pre_h, got = pre_got;
         first = false;
       } else {
-        got = ld_tagged(xo, g);
-        if (act) got = ld_tagged(xo + k, h2) && got;
+        got = ld_tagged(xo, g, false);
+        if (act) got = ld_tagged(xo + k, h2, false) && got;
       }
       if (__all(got || !ok)) {
+#ifdef AK_CHAIN_PROBE
+        if (b == 0) probe_wave(target, polls);
+#endif
         if (act) g = silu_mul8(g, h2);
         xv[b] = ok ? g : make_uint4(0u, 0u, 0u, 0u);
         break;
@@ -1106,8 +1133,9 @@ int m1d_tune_query(int bits, int m, const Segs& g, int k, int* split, int* nwv, 
 
 #ifdef AK_CHAIN_PROBE
 // the probe records and workgroup 0's flag word (a measurement build only)
-extern "C" int ak_chain_probe_read(void* host, size_t bytes, uint32_t* flag0) {
+extern "C" int ak_chain_probe_read(void* host, size_t bytes, uint32_t* flag0, void* waves) {
   int e = (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_probe), bytes, 0, hipMemcpyDeviceToHost);
+  if (!e) e = (int)hipMemcpyFromSymbol(waves, HIP_SYMBOL(g_probe_w), sizeof(g_probe_w), 0, hipMemcpyDeviceToHost);
   if (!e) e = (int)hipMemcpyFromSymbol(flag0, HIP_SYMBOL(g_chain_flags), 4, 0, hipMemcpyDeviceToHost);
   return e;
 }
