@@ -358,16 +358,23 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
   // a tagged step's activations of pass pass0 + b, reloaded until all of the wave's words carry the launch's tag (a
   // bounded wait: past it the chain's error flag is raised and the step goes on); one pass at a time, so that only
   // one pass's tagged words are held in registers
-  // (pre: the first attempt's words were requested by xpre, before the step's first weights: a step's last workgroup
-  // to start is the one the step waits for, and its activations must not return behind its own weight requests)
-  uint4 pre_g = make_uint4(0u, 0u, 0u, 0u), pre_h = pre_g;
-  bool pre_got = false;
+  // (pre: the first attempt's words of the first NPRE passes were requested by xpre, before the step's first
+  // weights: a step's last workgroup to start is the one the step waits for, and its activations must not return
+  // behind its own weight requests; two tokens take two passes at k = 5120)
+  constexpr int NPRE = MT == 1 ? 1 : 2;
+  uint4 pre_g[NPRE], pre_h[NPRE];
+  bool pre_got[NPRE];
   auto xpre = [&]() __attribute__((always_inline)) {
-    const int t = MT == 1 ? 0 : u0 / gpt, gk = (4 * q0 + u0 - t * gpt) * kG;
-    const bool ok = u0 < units && t < mm && gk < k;
-    if (wave * UPW < units) {
-      pre_got = ld_tagged(ok ? t * xk + gk : 0, pre_g, AK_TAG_CACHED_FIRST);
-      if (act) pre_got = ld_tagged((ok ? t * xk + gk : 0) + k, pre_h, AK_TAG_CACHED_FIRST) && pre_got;
+#pragma unroll
+    for (int b = 0; b < NPRE; ++b) {
+      const int u = u0 + b * ustride, t = MT == 1 ? 0 : u / gpt, gk = (4 * q0 + u - t * gpt) * kG;
+      const bool ok = u < units && t < mm && gk < k;
+      pre_g[b] = pre_h[b] = make_uint4(0u, 0u, 0u, 0u);
+      pre_got[b] = false;
+      if (b < npass && wave * UPW + b * ustride < units) {  // the wave has units in pass b (uniform)
+        pre_got[b] = ld_tagged(ok ? t * xk + gk : 0, pre_g[b], AK_TAG_CACHED_FIRST);
+        if (act) pre_got[b] = ld_tagged((ok ? t * xk + gk : 0) + k, pre_h[b], AK_TAG_CACHED_FIRST) && pre_got[b];
+      }
     }
   };
   auto xpoll = [&](int pass0, int b, bool pre) __attribute__((always_inline)) {
@@ -388,7 +395,7 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
       uint4 g, h2;
       bool got;
       if (first) {
-        g = pre_g, h2 = pre_h, got = pre_got;
+        g = pre_g[b < NPRE ? b : 0], h2 = pre_h[b < NPRE ? b : 0], got = pre_got[b < NPRE ? b : 0];
         first = false;
       } else {
         got = ld_tagged(xo, g, false);
@@ -409,14 +416,14 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
       __builtin_amdgcn_s_sleep(1);
     }
   };
-  // the activations of passes pass0 .. pass0 + XB - 1 (pre: pass 0, requested by xpre)
+  // the activations of passes pass0 .. pass0 + XB - 1 (pre: passes 0 .. NPRE - 1, requested by xpre)
   auto xload_wait = [&](int pass0, bool pre) __attribute__((always_inline)) {
     if (!tagged) {
       xload(pass0);
       return;
     }
 #pragma unroll
-    for (int b = 0; b < XB; ++b) xpoll(pass0, b, pre && b == 0);
+    for (int b = 0; b < XB; ++b) xpoll(pass0, b, pre && b < NPRE);
   };
   // a chained step that depends on earlier steps requests its first weights before it waits for them (below)
   const bool late_x = CHAIN && (wait || tagged);
