@@ -491,13 +491,24 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
   // ---- the first DEPTH items are requested, then step 2 of the activations: per group the limbs (to LDS), and in
   // meta the bias sums -OFF * sum(d_j) of the three limbs with the activation scale 2^(E - 148) as float bits
   if (wait && late_x && wave == 0) chain_poll(target);
+#ifndef AK_TAG_PREFETCH
+#define AK_TAG_PREFETCH 1
+#endif
+  // tagged: AK_TAG_PREFETCH of the DEPTH first items are requested before the activations are waited for, the rest
+  // after them (measured at M = 1: 1 of 2 about 0.4 % faster than 2 of 2, 0 of 2 1.5 % slower)
+  constexpr int NPF = AK_TAG_PREFETCH < DEPTH ? AK_TAG_PREFETCH : DEPTH;
   if (tagged) xpre();
 #pragma unroll
-  for (int d = 0; d < DEPTH; ++d) fetch_next(buf[d]);
+  for (int d = 0; d < DEPTH; ++d)
+    if (!tagged || d < NPF) fetch_next(buf[d]);
   if (late_x) {
     if (wait) lds_barrier();
     xload_wait(0, tagged);
     AK_PROBE(1);
+  }
+  if (tagged) {
+#pragma unroll
+    for (int d = NPF; d < DEPTH; ++d) fetch_next(buf[d]);
   }
 
   auto convert = [&](int p0) {
