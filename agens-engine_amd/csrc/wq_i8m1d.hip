@@ -144,15 +144,6 @@ __device__ __forceinline__ void probe_mark(uint32_t target, int i) {
 }
 #define AK_PROBE(i) \
   if constexpr (CHAIN) probe_mark(target, i)
-// per wave: the time its activations were ready and the polls it took
-__device__ unsigned long long g_probe_w[1024 * 256 * 16 * 2];
-__device__ __forceinline__ void probe_wave(uint32_t target, int polls) {
-  if ((threadIdx.x & 63) == 0 && blockIdx.x < 256) {
-    const size_t o = (((target & 1023u) * 256 + blockIdx.x) * 16 + (threadIdx.x >> 6)) * 2;
-    g_probe_w[o] = wall_clock64();
-    g_probe_w[o + 1] = (unsigned long long)polls;
-  }
-}
 #else
 #define AK_PROBE(i)
 #endif
@@ -385,13 +376,7 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
     const int xo = ok ? t * xk + gk : 0;
     const long long t0 = wall_clock64();
     bool first = pre;
-#ifdef AK_CHAIN_PROBE
-    int polls = 0;
-#endif
     for (;;) {
-#ifdef AK_CHAIN_PROBE
-      ++polls;
-#endif
       uint4 g, h2;
       bool got;
       if (first) {
@@ -402,9 +387,6 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
         if (act) got = ld_tagged(xo + k, h2, false) && got;
       }
       if (__all(got || !ok)) {
-#ifdef AK_CHAIN_PROBE
-        if (b == 0) probe_wave(target, polls);
-#endif
         if (act) g = silu_mul8(g, h2);
         xv[b] = ok ? g : make_uint4(0u, 0u, 0u, 0u);
         break;
@@ -1151,9 +1133,8 @@ int m1d_tune_query(int bits, int m, const Segs& g, int k, int* split, int* nwv, 
 
 #ifdef AK_CHAIN_PROBE
 // the probe records and workgroup 0's flag word (a measurement build only)
-extern "C" int ak_chain_probe_read(void* host, size_t bytes, uint32_t* flag0, void* waves) {
+extern "C" int ak_chain_probe_read(void* host, size_t bytes, uint32_t* flag0) {
   int e = (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_probe), bytes, 0, hipMemcpyDeviceToHost);
-  if (!e) e = (int)hipMemcpyFromSymbol(waves, HIP_SYMBOL(g_probe_w), sizeof(g_probe_w), 0, hipMemcpyDeviceToHost);
   if (!e) e = (int)hipMemcpyFromSymbol(flag0, HIP_SYMBOL(g_chain_flags), 4, 0, hipMemcpyDeviceToHost);
   return e;
 }
