@@ -350,3 +350,42 @@ def test_chain_tagged_and_barrier_waits_mix(m):
     plain = _run_mixed_chain(m, 1, False)
     for si, (g, w) in enumerate(zip(tagged[0], plain[0])):
         assert np.array_equal(g, w), f"step {'ABCDE'[si]}: tagged and barrier-only chains differ"
+
+
+def test_chain_tagged_read_of_a_later_segment():
+    """A: x -> (y0, y1, y2) in three segments; B reads y1 (segment 1: the tagged copy of a later segment); C reads
+    B's output with 2 tokens' rows as the step before it produced them.  Chained (with and without tagged
+    activations) equals one launch per step, on two runs in a row."""
+    K = kernels()
+    k, m = 2048, 2
+    a = [Lin(81 + i, n, k, 3) for i, n in enumerate((1024, 3072, 512))]
+    b, c = Lin(85, 2048, 3072, 4), Lin(87, 640, 2048, 2)
+    x = Dev(m * k * 2)
+    ya = [Dev(m * L.n * 2) for L in a]
+    yb, yc = Dev(m * 2048 * 2), Dev(m * 640 * 2)
+    steps = [wq_step(3, x, m, [L.L for L in a], ya, k), wq_step(4, ya[1], m, [b.L], [yb], 3072),
+             wq_step(2, yb, m, [c.L], [yc], 2048)]
+    for tags in ("1", "0"):
+        old = os.environ.get("AK_CHAIN_TAGS")
+        os.environ["AK_CHAIN_TAGS"] = tags
+        try:
+            ch = Chain(steps)
+        finally:
+            if old is None:
+                del os.environ["AK_CHAIN_TAGS"]
+            else:
+                os.environ["AK_CHAIN_TAGS"] = old
+        assert ch.chained
+        for rep in range(2):
+            xh = gen_x(900 + rep, m * k)
+            check(K.ak_memcpy_h2d(x.p, xh.ctypes.data, xh.nbytes), "h2d")
+            ch.run()
+            check(K.ak_synchronize(), "sync")
+            assert K.ak_wq_chain_status() == 0
+            got = [y.get(np.uint16, m * n) for y, n in ((yb, 2048), (yc, 640))]
+            gemv(3, x.p, m, [L.L for L in a], k, 128, ys=ya)
+            gemv(4, ya[1].p, m, [b.L], 3072, 128, ys=[yb])
+            gemv(2, yb.p, m, [c.L], 2048, 128, ys=[yc])
+            check(K.ak_synchronize(), "sync")
+            for g, (y, n, name) in zip(got, ((yb, 2048, "B"), (yc, 640, "C"))):
+                assert np.array_equal(g, y.get(np.uint16, m * n)), f"tags {tags} run {rep} step {name}"
