@@ -121,10 +121,11 @@ __device__ __attribute__((aligned(256))) uint32_t g_chain_flags[kChainMaxWg * kC
 __device__ uint32_t g_chain_err;
 
 // Tagged activations: where a step's x is the output of the step just before it, that step also writes its outputs
-// as 32-bit words (bf16 value | tag << 16, tag = the launch's 16-bit epoch) to a buffer of the chain, and the step
-// reads that buffer instead of waiting at the grid barrier: each wave loads its own activations device-coherently
-// until every word it holds carries the launch's tag.  One write-through and one read round trip then separate the
-// steps, instead of the write acknowledgement, the flag store, the poll and the activation read of the barrier.
+// as 32-bit words (bf16 value | tag << 16, tag = the low 16 bits of the chain's launch count + 1) to a buffer of the
+// chain, and the step reads that buffer instead of waiting at the grid barrier: each wave reads its own activations
+// (first through the L2, then device-coherently) until every word it holds carries the launch's tag.  One
+// write-through and one read round trip then separate the steps, instead of the write acknowledgement, the flag
+// store, the poll and the activation read of the barrier.
 // x complete means every workgroup of the step before has finished it (outputs are written at the end of a step, and
 // every output row is written); the host takes a tagged wait only where that step itself waited for the one before
 // it and the step after this one waits, so that the grid-barrier guarantee (every earlier step complete) still holds
