@@ -796,6 +796,10 @@ int plan_m1d(I8Args& a, int bits, int mt, bool chain, M1dShape& sh) {
     }
   }
   if (best > 1e29) return AK_INVALID;
+  // chained steps with at least 8 blocks per workgroup: whole blocks per wave (measured in the chained sweeps: M = 1
+  // 2937 -> 2918 us, M = 2 3840 -> 3782 us, one TP = 2 rank 2137 -> 2131 us; from 5 blocks on, TP = 2 got slower)
+  constexpr int kChainSplit1Blocks = 8;
+  if (chain && nbmax >= kChainSplit1Blocks) best_split = 1;
   // a measured pin (or the tuner's override) replaces the model's choice where the shape admits it
   const M1dPin* pin = find_pin(a, bits, mt);
   // (csplit 0: a chained launch keeps the model's split)
