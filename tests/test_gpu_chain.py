@@ -389,3 +389,34 @@ def test_chain_tagged_read_of_a_later_segment():
             check(K.ak_synchronize(), "sync")
             for g, (y, n, name) in zip(got, ((yb, 2048, "B"), (yc, 640, "C"))):
                 assert np.array_equal(g, y.get(np.uint16, m * n)), f"tags {tags} run {rep} step {name}"
+
+
+def test_chain_tag_wraps_after_65536_runs():
+    """The 16-bit launch tag of tagged activations wraps after 65536 launches of a chain: the runs around the wrap
+    (tag 65535, 0, 1) read their own activations, not the previous run's (each run gets new inputs; equal to one
+    launch per step)."""
+    K = kernels()
+    k = 1024
+    a, b = Lin(91, 1024, k, 3), Lin(93, 512, 1024, 4)
+    x = Dev(k * 2)
+    y1, y2 = Dev(1024 * 2), Dev(512 * 2)
+    ch = Chain([wq_step(3, x, 1, [a.L], [y1], k), wq_step(4, y1, 1, [b.L], [y2], 1024)])
+    assert ch.chained
+    xh = gen_x(950, k)
+    check(K.ak_memcpy_h2d(x.p, xh.ctypes.data, xh.nbytes), "h2d")
+    for _ in range(65534):  # runs 0 .. 65533 (tags 1 .. 65534)
+        ch.run()
+    check(K.ak_synchronize(), "sync")
+    assert K.ak_wq_chain_status() == 0
+    for rep in range(4):  # runs 65534 .. 65537: tags 65535, 0, 1, 2
+        xh = gen_x(951 + rep, k)
+        check(K.ak_memcpy_h2d(x.p, xh.ctypes.data, xh.nbytes), "h2d")
+        ch.run()
+        check(K.ak_synchronize(), "sync")
+        assert K.ak_wq_chain_status() == 0
+        got = [y1.get(np.uint16, 1024), y2.get(np.uint16, 512)]
+        gemv(3, x.p, 1, [a.L], k, 128, ys=[y1])
+        gemv(4, y1.p, 1, [b.L], 1024, 128, ys=[y2])
+        check(K.ak_synchronize(), "sync")
+        assert np.array_equal(got[0], y1.get(np.uint16, 1024)), f"run {65534 + rep}: step 0"
+        assert np.array_equal(got[1], y2.get(np.uint16, 512)), f"run {65534 + rep}: step 1"
