@@ -420,3 +420,46 @@ def test_chain_tag_wraps_after_65536_runs():
         check(K.ak_synchronize(), "sync")
         assert np.array_equal(got[0], y1.get(np.uint16, 1024)), f"run {65534 + rep}: step 0"
         assert np.array_equal(got[1], y2.get(np.uint16, 512)), f"run {65534 + rep}: step 1"
+
+
+def test_chain_in_a_graph_replays_with_new_inputs():
+    """The chained launch captured in a hipGraph (ak_wq_chain_run is capturable and allocates nothing): three replays,
+    each after new inputs were copied in with an eager synchronous copy, each equal to one launch per step (the launch
+    tag advances inside the kernel, so every replay reads its own tagged activations)."""
+    K = kernels()
+    hip = ctypes.CDLL("libamdhip64.so")
+    vp = ctypes.c_void_p
+    k = 2048
+    a, b, c = Lin(101, 2048, k, 3), Lin(103, 1024, 2048, 2), Lin(105, 768, 1024, 4)
+    x = Dev(k * 2)
+    y1, y2, y3 = Dev(2048 * 2), Dev(1024 * 2), Dev(768 * 2)
+    ch = Chain([wq_step(3, x, 1, [a.L], [y1], k), wq_step(2, y1, 1, [b.L], [y2], 2048),
+                wq_step(4, y2, 1, [c.L], [y3], 1024)])
+    assert ch.chained
+    stream, graph, exe = vp(), vp(), vp()
+    assert hip.hipStreamCreate(ctypes.byref(stream)) == 0
+    try:
+        assert hip.hipStreamBeginCapture(stream, ctypes.c_int(1)) == 0  # thread-local capture mode
+        rc = K.ak_wq_chain_run(ch.h, stream)
+        assert hip.hipStreamEndCapture(stream, ctypes.byref(graph)) == 0
+        check(rc, "ak_wq_chain_run under capture")
+        assert hip.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, ctypes.c_size_t(0)) == 0
+        for rep in range(3):
+            xh = gen_x(1100 + rep, k)
+            check(K.ak_memcpy_h2d(x.p, xh.ctypes.data, xh.nbytes), "h2d")
+            assert hip.hipGraphLaunch(exe, stream) == 0
+            assert hip.hipStreamSynchronize(stream) == 0
+            assert K.ak_wq_chain_status() == 0
+            got = [y.get(np.uint16, n) for y, n in ((y1, 2048), (y2, 1024), (y3, 768))]
+            gemv(3, x.p, 1, [a.L], k, 128, ys=[y1])
+            gemv(2, y1.p, 1, [b.L], 2048, 128, ys=[y2])
+            gemv(4, y2.p, 1, [c.L], 1024, 128, ys=[y3])
+            check(K.ak_synchronize(), "sync")
+            for g, (y, n, name) in zip(got, ((y1, 2048, "A"), (y2, 1024, "B"), (y3, 768, "C"))):
+                assert np.array_equal(g, y.get(np.uint16, n)), f"replay {rep} step {name}"
+    finally:
+        if exe:
+            hip.hipGraphExecDestroy(exe)
+        if graph:
+            hip.hipGraphDestroy(graph)
+        hip.hipStreamDestroy(stream)
