@@ -8,6 +8,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <atomic>
 #include <mutex>
 #include <new>
 
@@ -34,10 +35,13 @@ namespace {
 
 constexpr int kMaxTokensPerLaunch = 16;
 
-int g_mode = -1;  // -1: environment (AGENS_W4_EXACT=1 selects the exact path), 0: exact, 1: integer MFMA
+// Process-global switches (tuning and test selections, not per-call state): atomics, so that a switch set on one
+// thread while another launches is read whole; a launch sees the value set before it or after it.
+std::atomic<int> g_mode{-1};  // -1: environment (AGENS_W4_EXACT=1 selects the exact path), 0: exact, 1: integer MFMA
 
 bool exact_mode() {
-  if (g_mode >= 0) return g_mode == 0;
+  const int mode = g_mode.load(std::memory_order_relaxed);
+  if (mode >= 0) return mode == 0;
   static int env = -1;
   if (env < 0) {
     const char* v = getenv("AGENS_W4_EXACT");
@@ -47,19 +51,32 @@ bool exact_mode() {
 }
 
 // The smallest token count routed to the fp16-MFMA kernel (wq_mm.hip) in the default numerics: the measured crossover
-// with the integer-limb kernels (below it those are faster; see the design notes' crossover table).  0: never (the
-// integer numerics for every m, rows bit-identical for any m); set through ak_wq_set_mm_min or AGENS_WQ_MM_MIN.
-constexpr int kMmMinDefault = 9;
-int g_mm_min = -1;
+// with the integer-limb kernels (below it those are faster).  Both compute the same numerics bit for bit, so the
+// switch changes speed only.  0: never; set through ak_wq_set_mm_min or AGENS_WQ_MM_MIN.  Above kMmMaxK inputs the
+// integer kernels stay faster at every token count (measured: down 5120 x 27648 at 24..128 tokens).
+constexpr int kMmMinDefault = 17;
+constexpr int kMmMaxK = 8192;
+std::atomic<int> g_mm_min{-1};
 
-int mm_min() {
-  if (g_mm_min >= 0) return g_mm_min;
+// the explicit crossover (ak_wq_set_mm_min, else AGENS_WQ_MM_MIN), or -1 for the compiled-in rule
+int mm_min_set() {
+  const int v = g_mm_min.load(std::memory_order_relaxed);
+  if (v >= 0) return v;
   static int env = -2;
   if (env == -2) {
-    const char* v = getenv("AGENS_WQ_MM_MIN");
-    env = v && v[0] ? atoi(v) : -1;
+    const char* e = getenv("AGENS_WQ_MM_MIN");
+    env = e && e[0] ? atoi(e) : -1;
   }
-  return env >= 0 ? env : kMmMinDefault;
+  return env;
+}
+
+// whether a default-numerics call of m tokens takes the fp16-MFMA kernel (the kernel itself takes group 128 only): an
+// explicit crossover applies at every k, the compiled-in one up to kMmMaxK inputs
+bool mm_route(int m, int k, int group, bool exact) {
+  if (exact || group != 128) return false;
+  const int set = mm_min_set();
+  if (set >= 0) return set > 0 && m >= set;
+  return m >= kMmMinDefault && k <= kMmMaxK;
 }
 
 bool group_ok(int k, int group) { return (group == 64 || group == 128) && k % group == 0 && k % 32 == 0; }
@@ -122,8 +139,7 @@ int gemv(int bits, const void* x, int m, int nseg, const void* const* wt, const 
     if (n[i] < 1 || !wt[i] || !st[i] || !y[i] || (ldy && ldy[i] < n[i])) return AK_INVALID;
   const bool exact = bf16w || (!force_default && exact_mode());
   if (act && exact) return AK_INVALID;  // the fused activation is in the default path's kernels only
-  const int mmin = mm_min();
-  if (!exact && mmin > 0 && m >= mmin) {  // above the crossover: the fp16-MFMA kernel, all tokens at once
+  if (mm_route(m, k, group, exact)) {  // above the crossover: the fp16-MFMA kernel, all tokens at once
     const int e = mm_gemv(bits, x, m, make_segs(nseg, wt, st, y, n, ldy, 16), k, group, s, act);
     if (e != AK_INVALID) return e;
   }
@@ -165,15 +181,18 @@ int run_step(const ak_wq_step& st, hipStream_t s) {
 
 // ---- the entry point that allocates nothing: split-K partials and counters in a static device array
 //
-// Bytes of split-K scratch any route of one launch of at most 16 tokens can ask for: 4 KB of row-range counters,
-// then P (<= 8) stripe partials per token (padded to T = 4, 8 or 16: the kernels' token groups) per output row (padded
-// to 16-row blocks), 4 bytes each; chunks of 16 tokens reuse it in stream order.
+// Bytes of split-K scratch the call's route can ask for: 4 KB of row-range counters, then P (<= 8) stripe partials per
+// token per output row (rows padded to 16-row blocks), 4 bytes each.  Tokens per launch: the integer kernels take at
+// most 16 (padded to T = 4, 8 or 16: their token groups), the fp16-MFMA route (default numerics, group 128, m at or
+// above its crossover) 16 or 32 (one or two 16-token tiles); chunks of tokens reuse the scratch in stream order.
 constexpr size_t kNoAllocScratchBytes = (size_t)64 << 20;
 __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 
-size_t noalloc_scratch_need(int m, int nseg, const int* n, int k) {
+size_t noalloc_scratch_need(int m, int nseg, const int* n, int k, int group, int bf16w) {
   const int tiles = kpad(k) / 1024, P = tiles < 8 ? tiles : 8;
-  const int mm = m < 16 ? m : 16, T = mm <= 4 ? 4 : mm <= 8 ? 8 : 16;
+  const bool mm = mm_route(m, k, group, bf16w || exact_mode());
+  const int mt = m < 16 ? m : 16;
+  const int T = mm ? (m <= 16 ? 16 : 32) : mt <= 4 ? 4 : mt <= 8 ? 8 : 16;
   size_t blocks = 0;
   for (int i = 0; i < nseg; ++i) blocks += (size_t)(n[i] + 15) / 16;
   return 4096 + (size_t)P * T * blocks * 16 * 4;
@@ -231,7 +250,7 @@ int ak_wq_gemv_kt_multi_noalloc(int bits, const void* x, int m, int nseg, const 
   if (nseg < 1 || nseg > kMaxSegs || !n || m < 1 || k < 1) return AK_INVALID;
   for (int i = 0; i < nseg; ++i)
     if (n[i] < 1) return AK_INVALID;
-  if (noalloc_scratch_need(m, nseg, n, k) > kNoAllocScratchBytes) return AK_INVALID;
+  if (noalloc_scratch_need(m, nseg, n, k, group, bf16w) > kNoAllocScratchBytes) return AK_INVALID;
   const hipStream_t s = static_cast<hipStream_t>(stream);
   void* p = nullptr;
   if (const int e = noalloc_scratch(s, &p)) return e;
@@ -335,12 +354,11 @@ int ak_wq_chain_create(const ak_wq_step* steps, int nsteps, void** chain) {
     return AK_OOM;
   }
   memcpy(c->steps, steps, sizeof(ak_wq_step) * (size_t)nsteps);
-  // the chained kernel computes the integer numerics: a step that one launch would route to the fp16-MFMA kernel
-  // (m at or above its crossover) makes the chain run one launch per step, so that both give the same bits
+  // the chained kernel takes default-numerics steps of group 128 and at most two tokens (the same bits as one launch
+  // per step); any other chain runs one launch per step
   bool chainable = !exact_mode();
-  const int mmin = mm_min();
   for (int i = 0; i < nsteps && chainable; ++i)
-    chainable = steps[i].bf16w == 0 && steps[i].group == 128 && steps[i].m <= 2 && (mmin <= 0 || steps[i].m < mmin);
+    chainable = steps[i].bf16w == 0 && steps[i].group == 128 && steps[i].m <= 2;
   if (chainable) {
     int* ib = static_cast<int*>(malloc(sizeof(int) * 5 * (size_t)nsteps));
     const void** xs = static_cast<const void**>(malloc(sizeof(void*) * (size_t)nsteps));
@@ -412,12 +430,12 @@ int ak_wq_tune_query(int bits, int m, int nseg, const int* n, int k, int* split,
 }
 
 int ak_wq_set_mm_min(int m) {
-  g_mm_min = m < 0 ? -1 : m;
+  g_mm_min.store(m < 0 ? -1 : m, std::memory_order_relaxed);
   return 0;
 }
 
 int ak_w4_set_mma(int mode) {
-  g_mode = mode < 0 ? -1 : (mode ? 1 : 0);
+  g_mode.store(mode < 0 ? -1 : (mode ? 1 : 0), std::memory_order_relaxed);
   return 0;
 }
 // reference: selects a bit-identical sm90 kernel variant; one default kernel family here, so accepted and ignored

@@ -33,6 +33,7 @@
 // the load offsets are a fixed per-lane part plus a scalar part of (block, tile), the cursors advance by selects,
 // and a stripe that ends inside the group only leaves a copy of its accumulators; the group's epilogue turns those
 // into stripe partials.
+#include <atomic>
 #include <stdlib.h>
 
 #include <vector>
@@ -141,18 +142,6 @@ constexpr uint32_t kTagMask = 0xFFFFu;
 #define AK_TAG_PREFETCH 1
 #endif
 
-// AK_CHAIN_PROBE builds only (a measurement build, not the library): per step and workgroup, the wall-clock times of
-// the step's start, its activations ready, converted, the item loop done, the outputs issued and the step's end
-#ifdef AK_CHAIN_PROBE
-__device__ unsigned long long g_probe[1024 * 256 * 6];
-__device__ __forceinline__ void probe_mark(uint32_t target, int i) {
-  if (threadIdx.x == 0 && blockIdx.x < 256) g_probe[((target & 1023u) * 256 + blockIdx.x) * 6 + i] = wall_clock64();
-}
-#define AK_PROBE(i) \
-  if constexpr (CHAIN) probe_mark(target, i)
-#else
-#define AK_PROBE(i)
-#endif
 
 // Wave 0 polls until the flags of workgroups [0, nwg) are all at least `target` (wrap-safe).  It polls before it
 // requests weights of its own, so that no poll waits behind them.
@@ -489,7 +478,6 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
   if (late_x) {
     if (wait) lds_barrier();
     xload_wait(0, tagged);
-    AK_PROBE(1);
   }
   if (tagged) {
 #pragma unroll
@@ -522,7 +510,6 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
     convert(p0);
   }
   __syncthreads();
-  AK_PROBE(2);
 
   // A role: group c >> 2, limb c & 3 (limb 3 reads zeros), chunk 4 * (c >> 2) + h of the quad; half 1 is kCPQ * 48
   // bytes further
@@ -658,7 +645,6 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
     }
   }
   __syncthreads();
-  AK_PROBE(3);
   if constexpr (SK) {
     // every wave's partial stores are acknowledged at device scope before the range's counter moves
     __builtin_amdgcn_s_waitcnt(kVmcnt0);
@@ -671,7 +657,6 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
     }
     __syncthreads();
     if (!*last) {
-      AK_PROBE(4);
       return;
     }
     for (int i = tid; i < MT * nb * 4; i += 64 * nwv) {
@@ -693,7 +678,6 @@ __device__ __forceinline__ void m1d_body(const I8Args& a, uint8_t* lds, bool wai
         yseg[(size_t)t * ldy + row] = yl[i];
     }
   }
-  AK_PROBE(4);
 }
 
 template <int BITS, int SPLIT, int DEPTH, int MT, bool SK = false, bool ACT = false>
@@ -726,9 +710,11 @@ struct M1dPin {
 };
 #include "wq_launch_table.h"
 
+// The tuner's process-global override (ak_wq_tune_override): atomics, so that a launch on another thread reads each
+// field whole (tuning only: a launch during a change may see some fields before it and some after it)
 struct TuneOverride {
-  int split = 0, nwv = 0, sk = -1;  // 0 / -1: not overridden
-  bool nopins = false;              // the cost model alone (the tuner's reference)
+  std::atomic<int> split{0}, nwv{0}, sk{-1};  // 0 / -1: not overridden
+  std::atomic<bool> nopins{false};            // the cost model alone (the tuner's reference)
 };
 TuneOverride g_tune;
 
@@ -805,8 +791,9 @@ int plan_m1d(I8Args& a, int bits, int mt, bool chain, M1dShape& sh) {
   // a measured pin (or the tuner's override) replaces the model's choice where the shape admits it
   const M1dPin* pin = find_pin(a, bits, mt);
   // (csplit 0: a chained launch keeps the model's split)
-  const int want_split = g_tune.split ? g_tune.split : pin ? (chain ? pin->csplit : pin->split) : 0;
-  const int want_nwv = g_tune.nwv ? g_tune.nwv : pin ? pin->nwv : 0;
+  const int o_split = g_tune.split.load(std::memory_order_relaxed), o_nwv = g_tune.nwv.load(std::memory_order_relaxed);
+  const int want_split = o_split ? o_split : pin ? (chain ? pin->csplit : pin->split) : 0;
+  const int want_nwv = o_nwv ? o_nwv : pin ? pin->nwv : 0;
   if (want_split || want_nwv) {
     const int sp = want_split ? want_split : best_split, nw = chain ? 16 : want_nwv ? want_nwv : best_nwv;
     const bool ok = (sp == 1 || sp == 2 || sp == 4 || sp == 8) && sp <= a.P && (nw == 16 || nw == 8) &&
@@ -916,9 +903,6 @@ __global__ void __launch_bounds__(1024, 1) i8_chain_kernel(const ChainStep* __re
     const ChainStep st = steps[s];  // a copy: the step's fields live in scalar registers
     const bool w = st.wait != 0;
     const uint32_t target = f0 + (uint32_t)s;
-#ifdef AK_CHAIN_PROBE
-    probe_mark(target, 0);
-#endif
     switch (st.kind) {
       case 4 * 16 + 1: m1d_body<4, 1, D, MT, true>(st.a, lds, w, target, tag); break;
       case 4 * 16 + 2: m1d_body<4, 2, D, MT, true>(st.a, lds, w, target, tag); break;
@@ -949,9 +933,6 @@ __global__ void __launch_bounds__(1024, 1) i8_chain_kernel(const ChainStep* __re
     } else {
       lds_barrier();
     }
-#ifdef AK_CHAIN_PROBE
-    probe_mark(target, 5);
-#endif
   }
   if (threadIdx.x == 0) epochs[blockIdx.x] = ep + 1u;
 }
@@ -1084,7 +1065,7 @@ int m1d_chain_make(int nsteps, const int* bits, const void* const* x, const int*
   if (!e) e = (int)hipMemcpy(d, h, (size_t)nsteps * sizeof(ChainStep), hipMemcpyHostToDevice);
   free(h);
   if (e) {
-    if (d) hipFree(d);
+    if (d) (void)hipFree(d);
     return e == (int)hipErrorOutOfMemory ? AK_OOM : e;
   }
   *table = d;
@@ -1137,15 +1118,6 @@ int m1d_tune_query(int bits, int m, const Segs& g, int k, int* split, int* nwv, 
   *split = sh.split, *nwv = sh.nwv, *sk = 0;
   return 0;
 }
-
-#ifdef AK_CHAIN_PROBE
-// the probe records and workgroup 0's flag word (a measurement build only)
-extern "C" int ak_chain_probe_read(void* host, size_t bytes, uint32_t* flag0) {
-  int e = (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_probe), bytes, 0, hipMemcpyDeviceToHost);
-  if (!e) e = (int)hipMemcpyFromSymbol(flag0, HIP_SYMBOL(g_chain_flags), 4, 0, hipMemcpyDeviceToHost);
-  return e;
-}
-#endif
 
 // reads and clears the flag a chained launch raises when a wait ran out (0.2 s): 1 if one did since the last call
 int m1d_chain_error(int* err) {

@@ -2,19 +2,18 @@
 // ak_wq_gemv_kt_multi above its measured crossover in m (the role of the reference's tensor-core kernels for m > 1,
 // kernels/src/w4_gemv.cu:990-1163: bf16 MMA over the expanded codes, fp32 accumulation).
 //
-// Numerics ("MFMA numerics" of this route): per (token, group) the activations enter v_mfma_f32_16x16x32_f16 as fp16
-// scaled by a power of two, x * 2^s with s = min(141 - E, 126) (E = the group's largest bf16 exponent field: the
-// largest magnitude lands in [2^14, 2^15)), which is exact for every input within 2^28 of the group's largest (smaller
-// ones round toward zero in fp16's subnormal range); a stored code n enters as the exact fp16 q = (1024 + n) -
-// (1024 + OFF) (OFF = 8 / 4 / 2): one byte permute (bit pattern 0x6400 | n) and one packed fp16 subtraction per pair
-// of codes, from the int8 codes that make_b produces.  D_g = (chain of k-steps 0, 2) + (chain of k-steps 1, 3), each
-// a chain of 32-input MFMAs from zero (exact products, fp32 accumulation); acc = fmaf(D_g * 2^-s, scale_g, acc) over
-// a stripe's groups in order -- the reference tensor-core kernel's per-group form (w4_gemv.cu:1044-1052: exact q in the MMA, fmaf of the group sum with
-// the scale) -- with stripes as the integer numerics (P = min(8, #tiles) contiguous runs of whole 1024-input tiles),
-// y = stripe partials added left to right, bf16 RNE.  The MFMA computes each output element from its own A row and B
-// column, so a token's outputs do not depend on the other tokens of the launch, and every launch shape (split-K or
-// not, chunks, blocks per wave) gives the same bits.  A group holding an Inf or NaN: its finite inputs scale to zero
-// and the token's outputs take the Inf / NaN an fp32 path gives (Inf * q, NaN for Inf * 0).
+// Numerics: the default numerics of the integer-limb kernels (wq_i8_common.h), bit for bit, so that a token's outputs
+// are the same whichever kernel a launch takes and however many tokens share it (the reference's contract for batched
+// rows, w4_gemv.cu:1075-1079).  Per (token, group): E = the group's largest bf16 exponent field, x_int =
+// trunc(x * 2^(148 - E)) (|x_int| < 2^22), entered into v_mfma_f32_16x16x32_f16 as two exact fp16 limbs, hi = x_int >> 11
+// in [-2048, 2048) and lo = x_int & 2047; a stored code n enters as the exact fp16 q = (1024 + n) - (1024 + OFF)
+// (OFF = 8 / 4 / 2: one byte permute, bit pattern 0x6400 | n, and one packed fp16 subtraction per pair of codes).
+// Every product and partial sum of a group is an integer below 2^21, so each limb's chain of four MFMAs gives its
+// exact integer sum, and gsum = fmaf(D_hi, 2048, D_lo) = fp32_rn(sum(x_int * q)), the integer kernels' group sum.
+// Then acc[s] = fmaf(gsum, scale * 2^(E - 148), acc[s]) with s = the group's slot in its quad (g mod 4), a stripe's
+// partial = ((acc[0] + acc[1]) + acc[2]) + acc[3], stripes P = min(8, #tiles) contiguous runs of whole 1024-input
+// tiles, y = stripe partials added left to right, bf16 RNE.  A group holding an Inf or NaN: as the integer kernels
+// (act_scale_bits, x_int).
 //
 // MFMA layout (16-row blocks, one group of 128 inputs per chain of four MFMAs, 16 tokens per token tile):
 //   A = activations: lane (c, h) = (lane % 16, lane / 16) holds token c of the tile, slots 8 h .. 8 h + 7 of the k-step;
@@ -52,7 +51,8 @@ constexpr int kG = 128;
 constexpr int kRsrcWord3 = 0x00020000;  // raw buffer resource, dword 3 (CDNA)
 constexpr int kNt = 2;                    // streaming (non-temporal) cache policy for the weights
 constexpr int kVmcnt0 = 0x0F70;            // s_waitcnt immediate: vector memory counter 0, the others unconstrained
-constexpr int kMaxTok = 64;               // tokens per launch (4 token tiles)
+constexpr int kMaxTok = 32;               // tokens per launch (2 token tiles: two limb images of 64 tokens leave no room
+                                          // for two quads in the LDS)
 constexpr size_t kLds = 160 * 1024;
 constexpr int kZeros = 1024;  // LDS bytes of zeros at the start: A and C operands of a dummy item
 
@@ -108,11 +108,6 @@ __device__ __forceinline__ f16x8 mm_b(const i32x4& b0, const i32x4& b1, int j) {
   f16x8 r;
   __builtin_memcpy(&r, &v, 16);
   return r;
-}
-
-// fp32 of bf16 input i of the 16 dwords X (dword i / 2, low half first)
-__device__ __forceinline__ float x_at(const uint32_t (&X)[16], int i) {
-  return __uint_as_float((i & 1) ? (X[i >> 1] & 0xFFFF0000u) : (X[i >> 1] << 16));
 }
 
 // waves per workgroup: 16 for one token tile; 8 for more (their accumulators need the registers of two waves)
@@ -173,10 +168,11 @@ __global__ void __launch_bounds__(mm_waves<NTT>() * 64, 1) mm_kernel(const MmArg
     return pa + __builtin_popcountll(m0) + __builtin_popcountll(m1);
   };
 
-  // LDS: zeros [kZeros B: the operands of dummy items] | image [cq * 4 groups][4 k-steps][4 chunks][tl tokens] x 16 B (fp16) | meta [cq * 4 groups][tl tokens]: -s (int)
+  // LDS: zeros [kZeros B: the operands of dummy items] | image [cq * 4 groups][2 limbs][4 k-steps][4 chunks][tl tokens] x 16 B
+  //      (fp16) | meta [cq * 4 groups][tl tokens]: the activation scale (fp32 bits)
   //      | outputs [nb][MP tokens][16 rows]: bf16 results (SK: fp32 stripe partials), written out after the loop (a
   //        global store among the streaming loads would make the compiler drain every load in flight)
-  const int gbytes = 16 * tl * 16;
+  const int ls = 16 * tl * 16, gbytes = 2 * ls;  // one limb's image of a group, both limbs
   uint8_t* const img = lds + kZeros;
   float* const meta = reinterpret_cast<float*>(img + (size_t)cq * 4 * gbytes);
   uint8_t* const outl = reinterpret_cast<uint8_t*>(meta + cq * 4 * tl);
@@ -220,22 +216,29 @@ __global__ void __launch_bounds__(mm_waves<NTT>() * 64, 1) mm_kernel(const MmArg
       int mxi = (int)mx;
       mxi = max(mxi, __shfl_xor(mxi, 16));
       mxi = max(mxi, __shfl_xor(mxi, 32));
-      const int e = mxi >> 7;
-      const int sh = 141 - e < 126 ? 141 - e : 126;  // x * 2^sh: the largest magnitude in [2^14, 2^15)
+      const XiScale xs = xi_scale(mxi >> 7);
       uint8_t* dst = img + (size_t)g * gbytes + ((size_t)hh * tl + t) * 16;
-      // the scaled inputs in the operand order
+      // x_int of each input in the operand order, as its two exact fp16 limbs: hi = x_int >> 11 in [-2048, 2048) (image
+      // 0), lo = x_int & 2047 (image 1, ls bytes further)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        uint32_t d[4];
+        uint32_t dh[4], dl[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const auto h2 = __builtin_amdgcn_cvt_pkrtz(ldexpf(x_at(X, mm_pos<BITS>(j, 2 * q)), sh),
-                                                     ldexpf(x_at(X, mm_pos<BITS>(j, 2 * q + 1)), sh));
-          __builtin_memcpy(&d[q], &h2, 4);
+          const int i0 = mm_pos<BITS>(j, 2 * q), i1 = mm_pos<BITS>(j, 2 * q + 1);
+          const int x0 = x_int((X[i0 >> 1] >> (16 * (i0 & 1))) & 0xFFFFu, xs);
+          const int x1 = x_int((X[i1 >> 1] >> (16 * (i1 & 1))) & 0xFFFFu, xs);
+          const auto hp = __builtin_amdgcn_cvt_pkrtz((float)(x0 >> 11), (float)(x1 >> 11));
+          const auto lp = __builtin_amdgcn_cvt_pkrtz((float)(x0 & 2047), (float)(x1 & 2047));
+          __builtin_memcpy(&dh[q], &hp, 4);
+          __builtin_memcpy(&dl[q], &lp, 4);
         }
-        if (tv) *reinterpret_cast<uint4*>(dst + (size_t)j * 4 * tl * 16) = make_uint4(d[0], d[1], d[2], d[3]);
+        if (tv) {
+          *reinterpret_cast<uint4*>(dst + (size_t)j * 4 * tl * 16) = make_uint4(dh[0], dh[1], dh[2], dh[3]);
+          *reinterpret_cast<uint4*>(dst + ls + (size_t)j * 4 * tl * 16) = make_uint4(dl[0], dl[1], dl[2], dl[3]);
+        }
       }
-      if (tv && hh == 0) reinterpret_cast<int*>(meta)[g * tl + t] = -sh;  // D * 2^-s: the group's sum
+      if (tv && hh == 0) reinterpret_cast<int*>(meta)[g * tl + t] = act_scale_bits(mxi);  // 2^(E - 148), NaN, Inf
     }
   };
 
@@ -295,13 +298,18 @@ __global__ void __launch_bounds__(mm_waves<NTT>() * 64, 1) mm_kernel(const MmArg
     }
   };
 
-  float acc[NBW][NTT][4], yrun[NBW][NTT][4];
+  // accumulators per (block, token tile, group slot s = group mod 4 of the quad, output element)
+  float acc[NBW][NTT][4][4], yrun[NBW][NTT][4];
 #pragma unroll
   for (int b = 0; b < NBW; ++b)
 #pragma unroll
     for (int t = 0; t < NTT; ++t)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[b][t][i] = 0.f, yrun[b][t][i] = 0.f;
+      for (int i = 0; i < 4; ++i) {
+        yrun[b][t][i] = 0.f;
+#pragma unroll
+        for (int sl = 0; sl < 4; ++sl) acc[b][t][sl][i] = 0.f;
+      }
 
   // A operand and C (meta) offsets of this lane: token c of a tile (a one-tile image narrower than 16 tokens: rows past
   // it read token 0, their results are not written)
@@ -329,32 +337,37 @@ __global__ void __launch_bounds__(mm_waves<NTT>() * 64, 1) mm_kernel(const MmArg
       // (a dummy item -- two blocks per wave only -- reads its operands from the zeros: k-step strides of zero)
       const bool dz = NBW == 2 && !ok;
       const int jst = dz ? 0 : 4 * TL * 16;
-      const uint8_t* ab = dz ? lds + lane * 16 : img + (size_t)g * 256 * tlr + ((size_t)h * tlr + a_tok) * 16;
+      const uint8_t* ab = dz ? lds + lane * 16 : img + (size_t)g * 2 * 256 * tlr + ((size_t)h * tlr + a_tok) * 16;
+      const int lst = dz ? 0 : 16 * TL * 16;  // limb 1's image
       const int* eb = dz ? reinterpret_cast<const int*>(lds) : reinterpret_cast<const int*>(meta) + g * tlr + m_tok;
-      // the group's B operands once (several tiles reuse them), and with several tiles every A operand of the group
-      // requested before the first MFMA (2 waves per SIMD: the LDS latency is hidden by requests in flight)
-      f16x8 B[4], A[NTT][4];
+      // per (tile, limb) one chain of four MFMAs from zero; k-step j's B operand is formed once and feeds both limbs'
+      // chains of every tile.  Every partial sum is an integer below 2^21 (|limb| <= 2048, |q| <= 8, 128 inputs), so
+      // the sums are exact
+      f32x4 D[NTT][2];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) B[j] = mm_b<BITS>(b0, b1, j);
+      for (int tt = 0; tt < NTT; ++tt) D[tt][0] = D[tt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int tt = 0; tt < NTT; ++tt)
+      for (int j = 0; j < 4; ++j) {
+        const f16x8 B = mm_b<BITS>(b0, b1, j);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) __builtin_memcpy(&A[tt][j], ab + (size_t)j * jst + tt * 256, 16);
+        for (int tt = 0; tt < NTT; ++tt)
+#pragma unroll
+          for (int l = 0; l < 2; ++l) {
+            f16x8 A;
+            __builtin_memcpy(&A, ab + (size_t)l * lst + (size_t)j * jst + tt * 256, 16);
+            D[tt][l] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, D[tt][l], 0, 0, 0);
+          }
+      }
 #pragma unroll
       for (int tt = 0; tt < NTT; ++tt) {
-        // two independent chains (k-steps 0, 2 and 1, 3), added at the end: half the dependent MFMA latency
-        f32x4 d = {0.f, 0.f, 0.f, 0.f}, e = {0.f, 0.f, 0.f, 0.f};
+        const f32x4 dh = D[tt][0], dl = D[tt][1];
+        const i32x4 xe = *reinterpret_cast<const i32x4*>(eb + 16 * tt);  // activation scale per token
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          if (j & 1)
-            e = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[tt][j], B[j], e, 0, 0, 0);
-          else
-            d = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[tt][j], B[j], d, 0, 0, 0);
+        for (int i = 0; i < 4; ++i) {
+          // the group sum sum(x_int * q) rounded once to fp32 (hi * 2048 exact inside the fma), times scale * 2^(E-148)
+          const float gsum = fmaf(dh[i], 2048.0f, dl[i]);
+          acc[b][tt][s][i] = fmaf(gsum, sc[s] * __int_as_float(xe[i]), acc[b][tt][s][i]);
         }
-        d += e;
-        const i32x4 xe = *reinterpret_cast<const i32x4*>(eb + 16 * tt);  // -s per token
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[b][tt][i] = fmaf(ldexpf(d[i], xe[i]), sc[s], acc[b][tt][i]);
       }
     }
     const int rq = q - qa;
@@ -365,13 +378,16 @@ __global__ void __launch_bounds__(mm_waves<NTT>() * 64, 1) mm_kernel(const MmArg
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int o = (bl * MP + 16 * tt + 4 * h + i) * 16 + c;
+          // the stripe's partial: its four group slots added in order
+          const float part = ((acc[b][tt][0][i] + acc[b][tt][1][i]) + acc[b][tt][2][i]) + acc[b][tt][3][i];
           if constexpr (SK) {
-            reinterpret_cast<float*>(outl)[o] = acc[b][tt][i];
+            reinterpret_cast<float*>(outl)[o] = part;
           } else {
-            yrun[b][tt][i] = ep == 0 ? acc[b][tt][i] : yrun[b][tt][i] + acc[b][tt][i];
+            yrun[b][tt][i] = ep == 0 ? part : yrun[b][tt][i] + part;
             if (ep == P - 1) reinterpret_cast<uint16_t*>(outl)[o] = f2bf(yrun[b][tt][i]);
           }
-          acc[b][tt][i] = 0.f;
+#pragma unroll
+          for (int sl = 0; sl < 4; ++sl) acc[b][tt][sl][i] = 0.f;
         }
     }
   };
@@ -478,7 +494,7 @@ void launch_nbw(const MmArgs& a, int nb, int grid, size_t smem, hipStream_t s) {
 }
 
 // image bytes of cq quads at token stride tl
-size_t mm_image_bytes(int cq, int tl) { return kZeros + (size_t)cq * 4 * (16 * tl * 16 + tl * 4); }
+size_t mm_image_bytes(int cq, int tl) { return kZeros + (size_t)cq * 4 * (2 * 16 * tl * 16 + tl * 4); }
 
 template <int BITS, int NTT>
 int launch_mm(MmArgs a, hipStream_t s) {
@@ -564,7 +580,7 @@ int launch_mm(MmArgs a, hipStream_t s) {
 
 }  // namespace
 
-// 1..128 tokens in launches of at most 64 (16, 32 or 64 per launch in the kernel), group 128; act = 1: x is the merged
+// 1..128 tokens in launches of at most 32 (one or two 16-token tiles per launch), group 128; act = 1: x is the merged
 // gate_up [m][2k] and the activations SiLU(gate) * up.  AK_INVALID if the shape does not suit the kernel (the caller
 // falls back).
 int mm_gemv(int bits, const void* x, int m, const Segs& g, int k, int group, hipStream_t s, int act) {
@@ -580,7 +596,7 @@ int mm_gemv(int bits, const void* x, int m, const Segs& g, int k, int group, hip
     a.k = k;
     a.nquad = kpad(k) / kG / 4;
     a.P = stripe_count(a.nquad, 2);
-    const int ntt = mm <= 16 ? 1 : mm <= 32 ? 2 : 4;
+    const int ntt = mm <= 16 ? 1 : 2;
     a.tl = ntt == 1 ? (mm <= 4 ? 4 : mm <= 8 ? 8 : 16) : 16 * ntt;
     a.cq = 1;
     a.part = nullptr;
@@ -593,10 +609,7 @@ int mm_gemv(int bits, const void* x, int m, const Segs& g, int k, int group, hip
       case 21: e = launch_mm<2, 1>(a, s); break;
       case 42: e = launch_mm<4, 2>(a, s); break;
       case 32: e = launch_mm<3, 2>(a, s); break;
-      case 22: e = launch_mm<2, 2>(a, s); break;
-      case 44: e = launch_mm<4, 4>(a, s); break;
-      case 34: e = launch_mm<3, 4>(a, s); break;
-      default: e = launch_mm<2, 4>(a, s); break;
+      default: e = launch_mm<2, 2>(a, s); break;
     }
     if (e) return e;
   }

@@ -76,7 +76,8 @@ int ak_w4g128_repack_kt(const int32_t* packed, const void* scales, void* wt, voi
  *               adds NaN; one holding an Inf (no NaN) adds S * scale * Inf, S the sum of sign(x) * q over its Infs
  *               (+-Inf, or NaN where S = 0: the fp32 path's value wherever the group's Inf products share a sign).
  *               Groups whose largest input is below about 2^-100 lose precision to the underflow of the fp32 scale
- *               product (absolute errors below 2^-100);
+ *               product (absolute errors below 2^-100), where the reference's fp32 per-group path
+ *               (reference.rs:53-71) keeps them;
  *   exact    -- the reference's fp32 FMA path, bit for bit (ak_w4_set_mma(0) or AGENS_W4_EXACT=1);
  *   bf16w=1  -- weights rounded to bf16(q * scale) first (Marlin numerics), always on the fp32 path. */
 int ak_wq_gemv_kt_multi(int bits, const void* x, int m, int nseg, const void* const* wt, const void* const* st,

@@ -2,7 +2,9 @@
  * kernels/include/agens_kernels.h:271-277 ak_w4g128_gemv_kt_tune / _variant and the launch pins of
  * tools/aot_pins_sm90.json, produced by kernels/bench/tune_w4.cu:1-91).  Every launch configuration gives the same
  * output bits; these only select among them.  Used by agens-engine_amd/tune_launch.py, which measures the candidates
- * and writes the compiled-in table (csrc/wq_launch_table.h) that ak_wq_gemv_kt_multi consults.  Not for engines. */
+ * and writes the compiled-in table (csrc/wq_launch_table.h) that ak_wq_gemv_kt_multi consults.  Not for engines:
+ * every switch here is process-global (it changes the launches of every thread until it is reset) and meant for
+ * tuning and tests. */
 #pragma once
 
 #ifdef __cplusplus
@@ -20,9 +22,10 @@ int ak_wq_tune_override(int split, int nwv, int sk);
 int ak_wq_tune_query(int bits, int m, int nseg, const int* n, int k, int* split, int* nwv, int* sk);
 
 /* The smallest token count (m) that ak_wq_gemv_kt_multi and its conveniences route to the fp16-MFMA kernel in the
- * default numerics (group 128): m >= this many tokens take it, fewer take the integer-limb kernels.  0: never (the
- * integer numerics for every m: rows bit-identical for any m); negative: the compiled-in measured crossover (or the
- * environment variable AGENS_WQ_MM_MIN).  Process-wide.  Always 0. */
+ * default numerics (group 128): m >= this many tokens take it, fewer take the integer-limb kernels, at every k.  0:
+ * never (the integer-limb kernels for every m); negative: the compiled-in measured rule (17 tokens and k <= 8192; or
+ * the environment variable AGENS_WQ_MM_MIN).  Both kernels compute the same numerics bit for bit, so this changes
+ * speed only.  Process-wide.  Always 0. */
 int ak_wq_set_mm_min(int m);
 
 #ifdef __cplusplus

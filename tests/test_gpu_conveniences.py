@@ -23,7 +23,7 @@ def gpu():
     n = ctypes.c_int(0)
     assert K.ak_device_count(ctypes.byref(n)) == 0 and n.value >= 1, "no GPU visible"
     K.ak_w4_set_mma(1)
-    K.ak_wq_set_mm_min(0)  # the integer numerics at every m: the subject of this module
+    K.ak_wq_set_mm_min(0)  # the integer-limb kernels at every m (the same numerics as the MFMA route)
     yield K
     K.ak_w4_set_mma(-1)
     K.ak_wq_set_mm_min(-1)

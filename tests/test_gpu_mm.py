@@ -1,12 +1,14 @@
 """The MFMA route of ak_wq_gemv_kt_multi (csrc/wq_mm.hip): the default numerics above the measured crossover in m.
 
-Its numerics (exact fp16 q and power-of-two-scaled fp16 activations in v_mfma_f32_16x16x32_f16, fp32 accumulation,
-fmaf of each group sum with its scale) have no bit-for-bit counterpart in the reference (whose tensor-core kernels'
-bits come from the H100 MMA instruction), so parity is against the reference CPU path restated in the oracle: the reference's bound
-|y - ref64| <= 1 bf16 ulp + 1e-5 * sum|x * w| (kernels/bench/test_w4.cu:123-141, with the fp32-accumulation term of
-an MMA route) against fp64, and the north-star tolerance against ora_gemv_ref_f32 (reference.rs:53-71): each output is
-one of the two bf16 neighbours of a value within 2e-3 relative of the fp32 reference.  Size-independent properties at
-the benchmark shapes: a token's outputs do not depend on the other tokens of the launch, on the segments launched with it, or on the token count.
+The route computes the integer numerics of the small-M kernels (x_int = trunc(x * 2^(148 - E)) per group, the exact
+integer group sum rounded once to fp32, scale * 2^(E - 148), four group-slot accumulators per stripe, stripes added
+left to right) with x_int fed to v_mfma_f32_16x16x32_f16 as two exact fp16 limbs, so every output must equal the
+oracle's ora_gemv_fast_kt bit for bit -- the same bits a launch of fewer tokens on the integer kernels gives, which
+is the reference's contract for batched rows (kernels/src/w4_gemv.cu:1075-1079).  Also checked: the reference's bound
+|y - ref64| <= 1 bf16 ulp + 1e-6 * sum|x * w| (kernels/bench/test_w4.cu:123-141) against fp64, and the north-star
+tolerance against ora_gemv_ref_f32 (reference.rs:53-71).  Size-independent properties at the benchmark shapes: a
+token's outputs do not depend on the other tokens of the launch, on the segments launched with it, or on the token
+count.
 """
 import ctypes
 
@@ -14,7 +16,7 @@ import numpy as np
 import pytest
 
 from _lib import (kernels, Dev, Linear, gemv, gen_container, gen_scales, gen_x, ora_ref_f32, ora_ref_f64, ulp_bf16,
-                  bf2f_array, check)
+                  bf2f_array, check, ora_repack, ora_fast)
 
 pytestmark = pytest.mark.gpu
 
@@ -47,18 +49,26 @@ def rows_of(L, r0, r1):
 
 
 def check_rows(y, x, m, L, r0, r1, what=""):
-    """y [m][n] (bf16 bits) rows r0..r1 against fp64 (reference bound) and fp32."""
+    """y [m][n] (bf16 bits) rows r0..r1: bit-exact against the oracle's default numerics, and against fp64 (reference
+    bound) and fp32."""
     p, s = rows_of(L, r0, r1)
     nr = r1 - r0
+    rc, wt, st = ora_repack(L.bits, p, s, nr, L.k, G)
+    assert rc == 0
+    want = ora_fast(L.bits, x, m, wt, st, nr, L.k, G)
+    got = np.ascontiguousarray(y[:, r0:r1])
+    if not np.array_equal(got, want):
+        bad = np.argwhere(got != want)[:4]
+        raise AssertionError(f"{what} rows {r0}..{r1}: {int(np.sum(got != want))} outputs differ from the oracle, "
+                             f"e.g. (token, row) {bad.tolist()}")
     ref64, mag = ora_ref_f64(x, m, p, s, nr, L.k, G)
     yy = y[:, r0:r1]
     err = np.abs(bf2f_array(yy).astype(np.float64) - ref64)
-    bound = ulp_bf16(ref64) + 1e-5 * mag
+    bound = ulp_bf16(ref64) + 1e-6 * mag
     assert np.all(err <= bound), f"{what} rows {r0}..{r1}: worst {np.max(err / bound):.3f} of the bound"
     ref32 = ora_ref_f32(x, m, p, s, nr, L.k, G).astype(np.float64)
-    # the north-star tolerance for an MFMA route: y is one of the two bf16 neighbours of a value within 2e-3 (relative,
-    # the measure of bench_gemv.cu:146-148) of the fp32 reference -- an fp32 sum in another order may round to the
-    # other neighbour
+    # the north-star tolerance: y is one of the two bf16 neighbours of a value within 2e-3 (relative, the measure of
+    # bench_gemv.cu:146-148) of the fp32 reference
     y64 = bf2f_array(yy).astype(np.float64)
     rel = (np.abs(y64 - ref32) - ulp_bf16(ref32)) / (np.abs(ref32) + 1e-2)
     assert np.max(rel) <= 2e-3, f"{what}: {np.max(rel):.2e}"

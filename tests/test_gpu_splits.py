@@ -27,7 +27,7 @@ def K():
     n = ctypes.c_int(0)
     assert K.ak_device_count(ctypes.byref(n)) == 0 and n.value >= 1, "no GPU visible"
     K.ak_wq_tune_override.argtypes = [ctypes.c_int] * 3
-    K.ak_wq_set_mm_min(0)  # the integer numerics at every m: the subject of this module
+    K.ak_wq_set_mm_min(0)  # the integer-limb kernels at every m (the same numerics as the MFMA route)
     yield K
     K.ak_wq_tune_override(0, 0, -1)
     K.ak_wq_set_mm_min(-1)
