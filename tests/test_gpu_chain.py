@@ -196,8 +196,9 @@ def test_chain_fallback_runs_steps_one_launch_each():
 @pytest.mark.parametrize("m", [1, 2])
 def test_chain_at_decode_shapes_matches_launches(m):
     """Two 32B-shaped layers (QKV 5120 -> 5120 + 2 x 1024, O, gate_up 5120 -> 55296, down 27648 -> 5120; the down
-    steps split k across workgroups): the chained launch equals one launch per step bit for bit, on two runs in a row
-    (the split's counters return to zero); the oracle is too slow at these sizes to run step by step."""
+    steps split k across workgroups): every chained step equals the oracle on its first, middle and last 64 rows of
+    every segment, fed with the activations that step read; the chained launch equals one launch per step bit for
+    bit, on two runs in a row (the split's counters return to zero)."""
     K = kernels()
     H, KV, INTER = 5120, 1024, 27648
     h, steps, flow = build(m, [3, 2], H, KV, INTER)
@@ -209,6 +210,13 @@ def test_chain_at_decode_shapes_matches_launches(m):
     check(K.ak_synchronize(), "sync")
     assert K.ak_wq_chain_status() == 0
     got = read_outputs(m, flow)
+    for si, (lins, xin, k, ys) in enumerate(flow):
+        xv = h_host if si == 0 else xin.get(np.uint16, m * k)
+        for j, l in enumerate(lins):
+            y = got[si][j].reshape(m, l.n)
+            for r0 in sorted({0, l.n // 2 - 32, l.n - 64}):
+                want = ora_fast(l.bits, xv, m, l.wt, l.st, l.n, k, l.group, rows=(r0, r0 + 64))[:, r0:r0 + 64]
+                assert np.array_equal(y[:, r0:r0 + 64], want), f"step {si} segment {j} rows {r0}..{r0 + 64}"
     zero_outputs(flow)
     ch.run()
     check(K.ak_synchronize(), "sync")

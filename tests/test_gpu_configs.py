@@ -118,17 +118,28 @@ def layer_bits(layer, seed=20261201):
     return 2 if u < 0.3 else (3 if u < 0.8 else 4)
 
 
-@pytest.mark.parametrize("m", [4, 16])
-def test_config4_two_layers_step_by_step(m):
+@pytest.mark.parametrize("m,bits,default_route", [(4, None, False), (16, None, False), (16, (2, 3, 4), True),
+                                                  (24, (2, 3, 4), True)])
+def test_config4_layers_step_by_step(m, bits, default_route):
     """QKV(x = h) -> O(x = q) -> gate_up(x = o) -> down(x = SiLU(gate) * up of gate_up) -> next layer's h, as one
     chain (ak_wq_chain_run) and as one launch per step; every step's outputs equal the oracle applied to the inputs
-    that step actually read."""
+    that step actually read.  Two layers of the benchmark's bit widths on the integer-limb kernels, and three layers
+    (W2, W3, W4) on the library's default routing: at 24 tokens QKV, O and gate_up take the fp16-MFMA kernel and down
+    (k = 27648) the integer kernels."""
     K = kernels()
+    if default_route:
+        K.ak_wq_set_mm_min(-1)
+    try:
+        run_layers(K, m, bits or [layer_bits(li) for li in range(2)])
+    finally:
+        K.ak_wq_set_mm_min(0)
+
+
+def run_layers(K, m, layer_bit_widths):
     steps, flow = [], []
     h = Dev(m * H * 2)
     x = h
-    for li in range(2):
-        b = layer_bits(li)
+    for li, b in enumerate(layer_bit_widths):
         s = 4000 + 50 * li
         eq2 = {4: 21.5, 3: 5.5, 2: 1.5}[b]  # scales ~ 1 / sqrt(k E[q^2]): activations stay about unit size
         qkv = [Lin(s, H, H, b, 1 / np.sqrt(H * eq2)), Lin(s + 2, KV, H, b, 1 / np.sqrt(H * eq2)),
@@ -159,9 +170,10 @@ def test_config4_two_layers_step_by_step(m):
             xv = xin.get(np.uint16, m * k)
         for l, y in zip(lins, got[si]):
             check_rows(l, xv, m, y.reshape(m, l.n), f"step {si} n={l.n} bits={l.bits} m={m}")
-    # outputs stay finite and non-trivial through the two layers
-    f = bf2f_array(got[-1][0])
-    assert np.all(np.isfinite(f)) and np.std(f) > 0.05
+    # outputs stay finite and non-trivial through the first two layers (the third layer's SiLU * up products may grow
+    # beyond bf16's range; the oracle checks above cover whatever values arise)
+    f = bf2f_array(got[7][0])
+    assert np.all(np.isfinite(f)) and np.std(f) > 0.05, (np.sum(~np.isfinite(f)), np.std(f[np.isfinite(f)]))
     # one launch per step: the same bits
     for lins, xin, k, ys, act in flow:
         for y in ys:
