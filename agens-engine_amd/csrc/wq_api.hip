@@ -227,6 +227,57 @@ int noalloc_scratch(hipStream_t s, void** out) {
   return 0;
 }
 
+// One chained launch at a time per device: the chained kernel's workgroups wait on the device's flag words, which
+// every chained launch on the device shares.  Launches on one stream are ordered by the stream; a launch on another
+// stream is refused (hipErrorNotReady) while the device's last chained launch, issued on a different stream, has not
+// finished.  Under stream capture nothing is checked or recorded (the graph's order is the caller's).
+struct ChainGuard {
+  static constexpr int kMaxDevices = 64;
+  struct Last {
+    hipStream_t stream = nullptr;
+    hipEvent_t done = nullptr;
+    bool recorded = false;
+  };
+  static std::mutex& mu() {
+    static std::mutex m;
+    return m;
+  }
+  static Last& last(int dev) {
+    static Last l[kMaxDevices];
+    return l[dev];
+  }
+  int dev = -1;
+  bool capturing = false;
+  std::unique_lock<std::mutex> lock;
+
+  int begin(hipStream_t s) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (const int e = (int)hipStreamIsCapturing(s, &cs)) return e;
+    capturing = cs != hipStreamCaptureStatusNone;
+    if (capturing) return 0;
+    if (const int e = (int)hipGetDevice(&dev)) return e;
+    if (dev < 0 || dev >= kMaxDevices) return AK_INVALID;
+    lock = std::unique_lock<std::mutex>(mu());
+    Last& l = last(dev);
+    if (l.recorded && l.stream != s) {
+      const hipError_t q = hipEventQuery(l.done);
+      if (q == hipErrorNotReady) return (int)hipErrorNotReady;
+      if (q != hipSuccess) return (int)q;
+    }
+    return 0;
+  }
+  int end(hipStream_t s) {
+    if (capturing) return 0;
+    Last& l = last(dev);
+    if (!l.done)
+      if (const int e = (int)hipEventCreateWithFlags(&l.done, hipEventDisableTiming)) return e;
+    if (const int e = (int)hipEventRecord(l.done, s)) return e;
+    l.stream = s;
+    l.recorded = true;
+    return 0;
+  }
+};
+
 }  // namespace
 }  // namespace agq
 
@@ -392,7 +443,12 @@ int ak_wq_chain_run(void* chain, void* stream) {
   if (!chain) return AK_INVALID;
   const Chain* c = static_cast<const Chain*>(chain);
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  if (c->table) return m1d_chain_launch(c->table, c->nsteps, c->mt, c->smem, s);
+  if (c->table) {
+    ChainGuard g;
+    if (const int e = g.begin(s)) return e;
+    const int e = m1d_chain_launch(c->table, c->nsteps, c->mt, c->smem, s);
+    return e ? e : g.end(s);
+  }
   for (int i = 0; i < c->nsteps; ++i)
     if (const int e = run_step(c->steps[i], s)) return e;
   return 0;

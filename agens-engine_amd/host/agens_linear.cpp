@@ -2,6 +2,7 @@
 #include "agens_linear.h"
 
 #include <algorithm>
+#include <cstring>
 #include <mutex>
 
 #include "agens_kernels.h"
@@ -212,5 +213,81 @@ int linear_shared(const void* x, int nl, const QuantLinear* const* lins, void* c
   }
   return 0;
 }
+
+LinearChain::~LinearChain() {
+  if (chain_) ak_wq_chain_destroy(chain_);
+}
+
+int LinearChain::push(int bits, int group, const void* x, int m, int k, int nseg, const void* const* wt,
+                      const void* const* st, void* const* y, const int* n, const int* ldy, int bf16w,
+                      bool independent, bool act) {
+  if (chain_ || nseg < 1 || nseg > 4 || m < 1 || m > 128) return 1;
+  ak_wq_step s;
+  std::memset(&s, 0, sizeof(s));
+  s.bits = bits, s.m = m, s.nseg = nseg, s.k = k, s.group = group, s.bf16w = bf16w;
+  s.x = x;
+  for (int i = 0; i < nseg; ++i) s.wt[i] = wt[i], s.st[i] = st[i], s.y[i] = y[i], s.n[i] = n[i], s.ldy[i] = ldy[i];
+  s.independent = independent ? 1 : 0;
+  s.act = act ? 1 : 0;
+  steps_.push_back(s);
+  return 0;
+}
+
+int LinearChain::add(const QuantLinear& t, const void* x, void* y, int m, int bf16w, bool independent, bool act) {
+  if (chain_ || t.np < 1 || t.np > 2 || m < 1 || m > 128 || (act && t.np != 1)) return 1;
+  for (int j = 0; j < t.np; ++j) {
+    const QuantPart& q = t.p[j];
+    const void* wt = q.wt;
+    const void* st = q.st;
+    void* yp = static_cast<uint16_t*>(y) + q.r0;
+    // the parts of one linear read the same x and write disjoint rows: the second does not wait for the first
+    if (const int e = push(q.bits, q.group, x, m, t.k, 1, &wt, &st, &yp, &q.n, &t.n, bf16w, j > 0 || independent, act))
+      return e;
+  }
+  return 0;
+}
+
+int LinearChain::add_shared(const void* x, int nl, const QuantLinear* const* lins, void* const* ys, const int* ns,
+                            int m, int k, int bf16w, bool independent) {
+  if (chain_ || nl < 1 || nl > 4 || !lins || !ys || !ns) return 1;
+  for (int j = 0; j < nl; ++j)
+    if (!lins[j] || lins[j]->n != ns[j] || lins[j]->k != k) return 1;
+  bool done[4] = {false, false, false, false};
+  bool first = true;
+  for (int j = 0; j < nl; ++j) {
+    if (done[j]) continue;
+    if (lins[j]->np != 1) {  // a multi-part linear: its own steps
+      done[j] = true;
+      if (const int e = add(*lins[j], x, ys[j], m, bf16w, !first || independent)) return e;
+      first = false;
+      continue;
+    }
+    const QuantPart& pj = lins[j]->p[0];
+    const void *wt[4], *st[4];
+    void* y[4];
+    int nn[4], ld[4], c = 0;
+    for (int i = j; i < nl; ++i) {
+      if (done[i] || lins[i]->np != 1) continue;
+      const QuantPart& pi = lins[i]->p[0];
+      if (pi.bits != pj.bits || pi.group != pj.group) continue;
+      wt[c] = pi.wt, st[c] = pi.st, y[c] = ys[i], nn[c] = ns[i], ld[c] = ns[i], ++c;
+      done[i] = true;
+    }
+    // every class reads the same x: only the first waits for the step before
+    if (const int e = push(pj.bits, pj.group, x, m, k, c, wt, st, y, nn, ld, bf16w, !first || independent, false))
+      return e;
+    first = false;
+  }
+  return 0;
+}
+
+int LinearChain::build() {
+  if (chain_ || steps_.empty()) return 1;
+  return ak_wq_chain_create(steps_.data(), (int)steps_.size(), &chain_);
+}
+
+int LinearChain::run(void* stream) { return chain_ ? ak_wq_chain_run(chain_, stream) : 1; }
+
+bool LinearChain::chained() const { return chain_ && ak_wq_chain_chained(chain_) == 1; }
 
 }  // namespace agens

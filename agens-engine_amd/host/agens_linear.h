@@ -6,6 +6,8 @@
 // same against this library.  Errors are thrown as agens::Error (the Rust side's anyhow::bail) where the reference
 // bails, and returned as the reference's integer codes where it returns them (linear, linear_shared).
 #pragma once
+#include "agens_kernels.h"
+
 #include <cstddef>
 #include <cstdint>
 #include <optional>
@@ -86,5 +88,44 @@ void set_prefill_route(int mode);
 // (outputs bit-identical to separate GEMVs), otherwise one linear() each.
 int linear_shared(const void* x, int nl, const QuantLinear* const* lins, void* const* ys, const int* ns, int m, int k,
                   int bf16w, void* stream);
+
+// A run of consecutive GEMV calls of a decode step as one chained launch (ak_wq_chain_*): the role of the reference's
+// captured decode graph whose GEMV kernels get programmatic-dependent-launch edges (runtime.cu:198-230 ak_graph_pdl,
+// agens_pdl.cuh:1-16), so that each GEMV streams its weights while the one before it finishes.  Each call appended
+// here is the linear() / linear_shared() call of the same arguments (same outputs, bit for bit); a step waits for the
+// step before it unless declared independent (it reads nothing the step before writes).  Up to 128 tokens (the
+// prefill route is not chained).  Not thread-safe; the buffers must stay valid while the chain is used.
+class LinearChain {
+ public:
+  LinearChain() = default;
+  LinearChain(const LinearChain&) = delete;
+  LinearChain& operator=(const LinearChain&) = delete;
+  ~LinearChain();
+  // linear(t, x, y, m, t.n, t.k, bf16w): one step per part (a second part reads the same x: independent of the first).
+  // act: x is the merged gate_up [m][2 * t.k] and the step's activations are SiLU(gate) * up (ak_wq_gemv_kt_silu;
+  // single-part linears, default numerics).  1 for a bad argument or after build().
+  int add(const QuantLinear& t, const void* x, void* y, int m, int bf16w = 0, bool independent = false,
+          bool act = false);
+  // linear_shared(x, nl, lins, ys, ns, m, k, bf16w): one step per (bits, group) class of the single-part linears (their
+  // segments in one launch), a multi-part linear as add().  1 for a bad argument or after build().
+  int add_shared(const void* x, int nl, const QuantLinear* const* lins, void* const* ys, const int* ns, int m, int k,
+                 int bf16w = 0, bool independent = false);
+  // ak_wq_chain_create over the steps: validates, allocates and uploads the step table (synchronous; not under stream
+  // capture).  0 or an error code.
+  int build();
+  // one launch on `stream` (one launch per step where the chained kernel does not take a step: group 64, more than two
+  // tokens, exact numerics); allocates nothing and can be captured.  hipErrorNotReady (600) while the device's last
+  // chained launch, issued on another stream, is still running (chained launches on one device share its flag words).
+  int run(void* stream);
+  // 1: runs as one chained launch, 0: as one launch per step (after build())
+  bool chained() const;
+  size_t steps() const { return steps_.size(); }
+
+ private:
+  int push(int bits, int group, const void* x, int m, int k, int nseg, const void* const* wt, const void* const* st,
+           void* const* y, const int* n, const int* ldy, int bf16w, bool independent, bool act);
+  std::vector<ak_wq_step> steps_;
+  void* chain_ = nullptr;
+};
 
 }  // namespace agens

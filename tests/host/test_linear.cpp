@@ -159,6 +159,97 @@ int main() {
   EXPECT(get(ya.ptr(), 64) == get(ra.ptr(), 64), "shared A == separate");
   EXPECT(get(yb.ptr(), 32) == get(rb.ptr(), 32), "shared B == separate");
   EXPECT(get(yc.ptr(), 48) == get(rc.ptr(), 48), "shared C == separate");
+  // ---- LinearChain: two decoder layers (qkv of mixed bits through add_shared, o, a two-part gate_up W3 | W2, down
+  // with the SiLU(gate) * up activation) as one chained launch, equal bit for bit to the same calls one at a time
+  // (linear_shared, linear, ak_wq_gemv_kt_silu); 1 and 2 tokens chained, 4 tokens one launch per step
+  {
+    const int H = 1024, KV = 256, I = 16384;  // the fused activation is chained on split-K down steps (k >= 16384)
+    struct Layer {
+      std::vector<KtPair> kt;
+      QuantLinear q, kk, v, o, gu, dn;
+    };
+    auto make_lin = [&](Layer& L, QuantLinear& t, int n, int kin, int bits) {
+      std::vector<uint8_t> p, sc;
+      container(n, kin, g, bits, p, sc);
+      L.kt.push_back(wq_upload_kt(bits, p, sc, n, kin, g));
+      t.n = n, t.k = kin, t.np = 1;
+      t.p[0] = {L.kt.back().first.ptr(), L.kt.back().second.ptr(), 0, n, g, bits};
+    };
+    Layer layers[2];
+    for (int li = 0; li < 2; ++li) {
+      Layer& L = layers[li];
+      L.kt.reserve(8);
+      make_lin(L, L.q, H, H, 3);
+      make_lin(L, L.kk, KV, H, 3);
+      make_lin(L, L.v, KV, H, 4);
+      make_lin(L, L.o, H, H, 4);
+      QuantLinear gate, up;
+      make_lin(L, gate, I, H, 3);
+      make_lin(L, up, I, H, 2);
+      L.gu.n = 2 * I, L.gu.k = H, L.gu.np = 2;
+      L.gu.p[0] = gate.p[0];
+      L.gu.p[1] = up.p[0];
+      L.gu.p[1].r0 = I;
+      make_lin(L, L.dn, H, I, li ? 2 : 3);
+    }
+    for (int m : {1, 2, 4}) {
+      std::vector<uint16_t> hh((size_t)m * H);
+      for (auto& v : hh) v = f2bf(-1.f + 2.f * (rnd() >> 8) / 16777216.f);
+      DeviceBuffer h = upload(hh.data(), hh.size() * 2);
+      // outputs: [run][layer] q, k, v, o, gate_up, down
+      std::vector<DeviceBuffer> out[2][2];
+      for (int r = 0; r < 2; ++r)
+        for (int li = 0; li < 2; ++li) {
+          for (int n : {H, KV, KV, H, 2 * I, H}) out[r][li].emplace_back((size_t)m * n * 2);
+        }
+      LinearChain ch;
+      const void* x = h.ptr();
+      for (int li = 0; li < 2; ++li) {
+        Layer& L = layers[li];
+        auto& o = out[0][li];
+        const QuantLinear* lins[3] = {&L.q, &L.kk, &L.v};
+        void* ys[3] = {o[0].ptr(), o[1].ptr(), o[2].ptr()};
+        const int ns[3] = {H, KV, KV};
+        EXPECT(ch.add_shared(x, 3, lins, ys, ns, m, H) == 0, "chain add_shared");
+        EXPECT(ch.add(L.o, o[0].ptr(), o[3].ptr(), m) == 0, "chain add o");
+        EXPECT(ch.add(L.gu, o[3].ptr(), o[4].ptr(), m) == 0, "chain add gate_up");
+        EXPECT(ch.add(L.dn, o[4].ptr(), o[5].ptr(), m, 0, false, true) == 0, "chain add down");
+        x = o[5].ptr();
+      }
+      EXPECT(ch.build() == 0, "chain build");
+      EXPECT(ch.chained() == (m <= 2), "chained for 1 and 2 tokens");
+      EXPECT(ch.add(layers[0].o, h.ptr(), out[0][0][3].ptr(), m) == 1, "add after build -> 1");
+      EXPECT(ch.run(nullptr) == 0, "chain run");
+      check(ak_synchronize(), "sync");
+      EXPECT(ak_wq_chain_status() == 0, "chain status");
+      // the same calls one at a time
+      x = h.ptr();
+      for (int li = 0; li < 2; ++li) {
+        Layer& L = layers[li];
+        auto& o = out[1][li];
+        const QuantLinear* lins[3] = {&L.q, &L.kk, &L.v};
+        void* ys[3] = {o[0].ptr(), o[1].ptr(), o[2].ptr()};
+        const int ns[3] = {H, KV, KV};
+        EXPECT(linear_shared(x, 3, lins, ys, ns, m, H, 0, nullptr) == 0, "linear_shared");
+        EXPECT(linear(L.o, o[0].ptr(), o[3].ptr(), m, H, H, 0, nullptr) == 0, "linear o");
+        EXPECT(linear(L.gu, o[3].ptr(), o[4].ptr(), m, 2 * I, H, 0, nullptr) == 0, "linear gate_up");
+        const QuantPart& d = L.dn.p[0];
+        EXPECT(ak_wq_gemv_kt_silu(d.bits, o[4].ptr(), m, d.wt, d.st, o[5].ptr(), H, 0, I, g, nullptr) == 0,
+               "silu gemv");
+        x = o[5].ptr();
+      }
+      bool same = true;
+      for (int li = 0; li < 2; ++li)
+        for (size_t i = 0; i < out[0][li].size(); ++i) {
+          const size_t cnt = out[0][li][i].bytes() / 2;
+          same = same && get(out[0][li][i].ptr(), cnt) == get(out[1][li][i].ptr(), cnt);
+        }
+      EXPECT(same, "chained steps == one call at a time");
+      // a second run on the same stream is ordered after the first: accepted
+      EXPECT(ch.run(nullptr) == 0, "second chain run");
+      check(ak_synchronize(), "sync");
+    }
+  }
   // ---- upload errors (lib.rs: size mismatch bails, W3 returns None on a 4-bit value, wq bails)
   std::vector<uint8_t> p4, s4;
   container(32, k, g, 4, p4, s4);

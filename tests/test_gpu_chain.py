@@ -471,3 +471,31 @@ def test_chain_in_a_graph_replays_with_new_inputs():
         if graph:
             hip.hipGraphDestroy(graph)
         hip.hipStreamDestroy(stream)
+
+
+def test_chained_launches_on_two_streams_are_refused_while_one_runs():
+    """Chained launches on one device share its flag words: ak_wq_chain_run refuses (hipErrorNotReady, 600) a launch on
+    another stream while the device's last chained launch is still running, and accepts launches on the same stream
+    (stream-ordered) and, once the other finished, on the other stream."""
+    K = kernels()
+    hip = ctypes.CDLL("libamdhip64.so")
+    sa, sb = ctypes.c_void_p(), ctypes.c_void_p()
+    assert hip.hipStreamCreate(ctypes.byref(sa)) == 0 and hip.hipStreamCreate(ctypes.byref(sb)) == 0
+    try:
+        k, n = 5120, 55296
+        big = Lin(61, n, k, 3)
+        x, y = Dev(k * 2), Dev(n * 2)
+        # 200 independent steps over one 106 MB weight: a few milliseconds of device time per run
+        steps = [wq_step(3, x, 1, [big.L], [y], k, independent=1) for _ in range(200)]
+        ch = Chain(steps)
+        assert ch.chained
+        assert K.ak_wq_chain_run(ch.h, sa) == 0
+        assert K.ak_wq_chain_run(ch.h, sb) == 600, "a chained launch on another stream while one runs"
+        assert K.ak_wq_chain_run(ch.h, sa) == 0, "the same stream is ordered: accepted"
+        assert hip.hipStreamSynchronize(sa) == 0
+        assert K.ak_wq_chain_run(ch.h, sb) == 0, "the other stream once the first launch finished"
+        assert hip.hipStreamSynchronize(sb) == 0
+        assert K.ak_wq_chain_status() == 0
+    finally:
+        hip.hipStreamDestroy(sa)
+        hip.hipStreamDestroy(sb)
