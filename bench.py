@@ -431,8 +431,10 @@ def run_xover(args, K, B):
                                  ctypes.POINTER(ctypes.c_float)]
     B.agb_time_xover.restype = ctypes.c_int
     ms_list = [1, 2, 4, 8, 16, 32, 64, 128, 256, 512]
+    K.ak_wq_set_mm_min.restype, K.ak_wq_set_mm_min.argtypes = ctypes.c_int, [ctypes.c_int]
     lines = []
-    for name, bits, n, k in (("gate_up_w3", 3, 55296, 5120), ("o_w4", 4, 5120, 5120), ("down_w2", 2, 5120, 27648)):
+    for name, bits, n, k in (("gate_up_w3", 3, 55296, 5120), ("o_w4", 4, 5120, 5120), ("down_w2", 2, 5120, 27648),
+                             ("qkv_w4", 4, 7168, 5120), ("lm_head_w4", 4, 152064, 5120)):
         lins = []
         while sum(L.wbytes for L in lins) < 400e6:
             lins.append(QLinear(ctx, SEED * 1000 + 700 + len(lins), n, k, bits))
@@ -451,6 +453,13 @@ def run_xover(args, K, B):
                 ctx.check(B.agb_time_xover(bits, x, m, wts, sts, len(lins), wd, y, n, k, 0, 3, 20, ctypes.byref(t)),
                           "gemv")
                 row["us_gemv"][m] = round(t.value * 1e3, 2)
+                if m >= 2:  # the two GEMV routes of the default numerics (bit-identical), each forced
+                    for key, mmin in (("us_gemv_integer", 0), ("us_gemv_mfma", 2)):
+                        K.ak_wq_set_mm_min(mmin)
+                        ctx.check(B.agb_time_xover(bits, x, m, wts, sts, len(lins), wd, y, n, k, 0, 3, 20,
+                                                   ctypes.byref(t)), "gemv route")
+                        row.setdefault(key, {})[m] = round(t.value * 1e3, 2)
+                    K.ak_wq_set_mm_min(-1)
             ctx.check(B.agb_time_xover(bits, x, m, wts, sts, len(lins), wd, y, n, k, 1, 2, 10, ctypes.byref(t)),
                       "dequant + gemm")
             row["us_dequant_gemm"][m] = round(t.value * 1e3, 2)

@@ -87,9 +87,10 @@ int ak_wq_gemv_kt_multi(int bits, const void* x, int m, int nseg, const void* co
  * (code under stream capture, tight serving loops, harnesses that forbid allocation).  Same arguments, results and
  * error codes; its split-K launches keep their partials and counters in a static 64 MiB device array of the library
  * (one per GPU, held until the process ends) instead of per-stream scratch.  Returns 1 when the call's worst-case
- * scratch, 4096 + 64 * P * T * sum_i ceil(n[i] / 16) bytes (P = min(8, ceil(k / 1024)), T = 4, 8 or 16 for up to 4,
- * 8 or more tokens), exceeds it (e.g. a 152064-row linear at more than 8 tokens).  Calls that overlap in time on one
- * GPU share the array and race: keep them on one stream. */
+ * scratch on its route, 4096 + 64 * P * T * sum_i ceil(n[i] / 16) bytes (P = min(8, ceil(k / 1024)); T = 4, 8 or 16
+ * for up to 4, 8 or 16 tokens on the integer kernels, 16 or 32 for up to 16 or more tokens on the fp16-MFMA route that
+ * the default numerics take from 17 tokens at k <= 8192), exceeds it (e.g. a 152064-row linear at more than 8 tokens).
+ * Calls that overlap in time on one GPU share the array and race: keep them on one stream. */
 int ak_wq_gemv_kt_multi_noalloc(int bits, const void* x, int m, int nseg, const void* const* wt,
                                 const void* const* st, void* const* y, const int* n, const int* ldy, int k, int group,
                                 int bf16w, void* stream);
@@ -206,7 +207,9 @@ int ak_wq_gemv_kt_silu(int bits, const void* gate_up, int m, const void* wt, con
  *   ak_wq_chain_create  validates the steps (as ak_wq_gemv_kt_multi: 1 on a bad argument), allocates and uploads the
  *                       chain's step table (device memory, synchronous); not under stream capture;
  *   ak_wq_chain_run     one launch on `stream`, allocates nothing, capturable; at most one chained launch may run on
- *                       a device at a time (they share the device's flag words);
+ *                       a device at a time (they share the device's flag words): outside capture, a launch on another
+ *                       stream than the device's last chained launch is refused with 600 (hipErrorNotReady) while that
+ *                       launch has not finished;
  *   ak_wq_chain_status  after the stream is synchronized: 1 if a chained launch's bounded wait (0.2 s) ran out since
  *                       the last call (its outputs are then not valid), else 0; negative: a HIP error. */
 typedef struct ak_wq_step {
