@@ -113,3 +113,30 @@ def test_nonfinite_and_subnormal_activations(bits, group, n, k, m):
             if t % 4 == 3:
                 err = np.abs(bf2f_array(y[t]).astype(np.float64) - ref64[t])
                 assert np.all(err <= 2.0 ** -100), f"{what}: subnormal token {t}: {err.max()}"
+
+
+@pytest.mark.parametrize("bits,n,k,m", [(3, 256, 5120, 16), (2, 300, 5120, 24), (4, 256, 3072, 40),
+                                        (3, 512, 27648, 17)])
+def test_nonfinite_on_the_mfma_route(bits, n, k, m):
+    """The fp16-MFMA route (forced from 2 tokens) on the same non-finite and subnormal activations: the oracle's bits
+    (NaN positions, every other output bit), as the integer kernels give them."""
+    K = kernels()
+    lo, span = -(1 << (bits - 1)), 1 << bits
+    packed = gen_container(7200 + bits, n, k, lo, span)
+    scales = gen_scales(7201 + bits, n * k // 128)
+    L = Linear(packed, scales, n, k, 128, bits)
+    check(L.rc)
+    wt, st = L.host_kt()
+    x = special_x(m, k, 128, 7300 + m)
+    X = Dev.of(x)
+    ys = {}
+    for mmin in (2, 0):
+        K.ak_wq_set_mm_min(mmin)
+        try:
+            (Y,) = gemv(bits, X, m, [L], k, 128)
+        finally:
+            K.ak_wq_set_mm_min(0)
+        ys[mmin] = Y.get(np.uint16, m * n).reshape(m, n)
+    what = f"MFMA route bits={bits} n={n} k={k} m={m}"
+    same_bits_nan_aware(ys[2], ora_fast(bits, x, m, wt, st, n, k, 128), what)
+    same_bits_nan_aware(ys[2], ys[0], what + " vs the integer kernels")
