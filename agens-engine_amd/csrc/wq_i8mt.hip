@@ -12,8 +12,9 @@
 //   D: lane (c, h) holds row c x token 4 tg + h, its three limb sums in D[0..2] and, through the C operand (meta), the
 //     bias -OFF * sum(d_j) and the token's activation scale in D[3] -- everything a lane needs stays in the lane.
 //
-// Loads: an item is 16 rows x one quad (512 inputs).  W4: one 16-byte chunk per group (16 rows x 64 B per instruction,
-// the four instructions of an item complete each row's two lines back to back).  W2 and the W3 two-bit planes: one
+// Loads: an item is 16 rows x one quad (512 inputs), loaded in whole lines (8 rows x 128 B per instruction: the two
+// lanes of a column pair load the two halves of one row's line, and one DPP swap per dword pair gives each lane its own
+// row, quad_pair_rows).  Then W4: one 16-byte chunk per group.  W2 and the W3 two-bit planes: one
 // 16-byte chunk pair per lane covers two groups (chunks 2 (h >> 1), 2 (h >> 1) + 1 of group 2 j + (h & 1)); one
 // v_permlane16_swap per dword pair (odd 16-lane rows of the first operand <-> even rows of the second) turns it into
 // the operands of groups 2 j and 2 j + 1.  The W3 third-bit plane the same with 8-byte pairs.
@@ -185,27 +186,28 @@ __global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
       const_cast<void*>(AK_PICK(sg, sgs.wt)), (short)0, ntile * n * REC, kRsrcWord3);
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(AK_PICK(sg, sgs.st)), (short)0, ntile * n * 16, kRsrcWord3);
-  // W2 / W3: the chunk pair 2 (h >> 1), 2 (h >> 1) + 1 of group 2 jj + (h & 1) (jj = 0, 1: 64 B of the row each)
-  const int cp = 4 * (h & 1) + 2 * (h >> 1);
-  const int vo_w = c * REC + (BITS == 4 ? h * 16 : cp * 8), vo_h = c * REC + 256 + cp * 4, vo_s = c * 16;
+  // pair loads (quad_vo_w / quad_vo_h): load e reads row 2 (c >> 1) + e, the even lane of a column pair the first half
+  // of each line, the odd lane the second; W2 / W3 after quad_pair_rows: the chunk pair 2 (h >> 1), 2 (h >> 1) + 1 of
+  // group 2 jj + (h & 1) in lo[jj]
+  const int vo_w = quad_vo_w(BITS, c, h, REC), vo_h = quad_vo_h(c, h, REC), vo_s = c * 16;
   const int tile_w = n * REC, tile_s = n * 16;
   auto fetch1 = [&](int blk, int qd, QuadRaw<BITS>& d) {
     const int row0 = (b_lo + blk) * 16, odd = qd & 1;
     const int so = row0 * REC + (qd >> 1) * tile_w;
     if constexpr (BITS == 4) {
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rw, vo_w, so + odd * 256 + s * 64, kNt);
+      for (int s = 0; s < 4; ++s) {  // line s >> 1 of row 2 (c >> 1) + (s & 1)
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rw, vo_w, so + odd * 256 + (s >> 1) * 128 + (s & 1) * REC, kNt);
         d.w[s] = make_uint4(v[0], v[1], v[2], v[3]);
       }
     } else {
 #pragma unroll
       for (int jj = 0; jj < 2; ++jj) {
-        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rw, vo_w, so + odd * 128 + jj * 64, kNt);
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rw, vo_w, so + odd * 128 + jj * REC, kNt);
         d.lo[jj] = make_uint4(v[0], v[1], v[2], v[3]);
         if constexpr (BITS == 3) {
           typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-          const u32x2 g2 = __builtin_amdgcn_raw_buffer_load_b64(rw, vo_h, so + odd * 64 + jj * 32, kNt);
+          const u32x2 g2 = __builtin_amdgcn_raw_buffer_load_b64(rw, vo_h, so + odd * 64 + jj * REC, kNt);
           d.hi[jj] = make_uint2(g2[0], g2[1]);
         }
       }
@@ -274,7 +276,7 @@ __global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
     for (int s = 0; s < 4; ++s) acc[t][s] = 0.f;
   }
   // one item without branches: an[][] = the accumulators before a stripe end reset them
-  auto core = [&](const QuadRaw<BITS>& bf, float (&an)[NT][4], bool& end, int& eg, int& ep) {
+  auto core = [&](QuadRaw<BITS>& bf, float (&an)[NT][4], bool& end, int& eg, int& ep) {
     const int r0 = cq - qa;
     end = ((r0 < 64 ? ends0 >> r0 : ends1 >> (r0 - 64)) & 1ull) != 0;
     // scales first: the loaded dwords die here (scales live to the end of the item would be copied at the loop latch)
@@ -284,6 +286,7 @@ __global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
     sc[2] = __uint_as_float(bf.s.y << 16);
     sc[3] = __uint_as_float(bf.s.y & 0xFFFF0000u);
     asm volatile("" ::"v"(sc[0]), "v"(sc[1]), "v"(sc[2]), "v"(sc[3]));
+    quad_pair_rows<BITS>(bf, (c & 1) != 0);  // in place: the buffer is refilled after the item
     Raw<BITS> rq[4];
     quad_groups<BITS>(bf, rq);
 #pragma unroll

@@ -249,8 +249,8 @@ __global__ void __launch_bounds__(mm_waves<NTT>() * 64, 1) mm_kernel(const MmArg
       const_cast<void*>(AK_PICK(sg, sgs.wt)), (short)0, ntile * n * REC, kRsrcWord3);
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(AK_PICK(sg, sgs.st)), (short)0, ntile * n * 16, kRsrcWord3);
-  const int cp = 4 * (h & 1) + 2 * (h >> 1);
-  const int vo_w = c * REC + (BITS == 4 ? h * 16 : cp * 8), vo_h = c * REC + 256 + cp * 4, vo_s = c * 16;
+  // pair loads (quad_vo_w / quad_vo_h): whole lines per instruction, each lane's own row after quad_pair_rows
+  const int vo_w = quad_vo_w(BITS, c, h, REC), vo_h = quad_vo_h(c, h, REC), vo_s = c * 16;
   const int tile_w = n * REC, tile_s = n * 16;
   auto fetch1 = [&](int blk, int qd, QuadRaw<BITS>& d) __attribute__((always_inline)) {
     const int row0 = (b_lo + blk) * 16, odd = qd & 1;
@@ -258,17 +258,17 @@ __global__ void __launch_bounds__(mm_waves<NTT>() * 64, 1) mm_kernel(const MmArg
     if constexpr (BITS == 4) {
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rw, vo_w, so + odd * 256 + s * 64, kNt);
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rw, vo_w, so + odd * 256 + (s >> 1) * 128 + (s & 1) * REC, kNt);
         d.w[s] = make_uint4(v[0], v[1], v[2], v[3]);
       }
     } else {
 #pragma unroll
       for (int jj = 0; jj < 2; ++jj) {
-        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rw, vo_w, so + odd * 128 + jj * 64, kNt);
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rw, vo_w, so + odd * 128 + jj * REC, kNt);
         d.lo[jj] = make_uint4(v[0], v[1], v[2], v[3]);
         if constexpr (BITS == 3) {
           typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-          const u32x2 g2 = __builtin_amdgcn_raw_buffer_load_b64(rw, vo_h, so + odd * 64 + jj * 32, kNt);
+          const u32x2 g2 = __builtin_amdgcn_raw_buffer_load_b64(rw, vo_h, so + odd * 64 + jj * REC, kNt);
           d.hi[jj] = make_uint2(g2[0], g2[1]);
         }
       }
@@ -318,13 +318,14 @@ __global__ void __launch_bounds__(mm_waves<NTT>() * 64, 1) mm_kernel(const MmArg
   // one item: block b (compile-time), quad q, chunk's first quad q0, local block bl.  A dummy item (ok = false: the
   // second block of a wave that has one) reads its A and C operands from the zeros, so that it adds exactly zero.  At a stripe end the partial (SK) or, at the
   // last stripe, the output is staged in LDS (no global access here: the loads stay exactly counted).
-  auto core = [&](const QuadRaw<BITS>& bf, auto bc, int q, int q0, bool ok, int bl) __attribute__((always_inline)) {
+  auto core = [&](QuadRaw<BITS>& bf, auto bc, int q, int q0, bool ok, int bl) __attribute__((always_inline)) {
     constexpr int b = decltype(bc)::value;
     float sc[4];
     sc[0] = __uint_as_float(bf.s.x << 16);
     sc[1] = __uint_as_float(bf.s.x & 0xFFFF0000u);
     sc[2] = __uint_as_float(bf.s.y << 16);
     sc[3] = __uint_as_float(bf.s.y & 0xFFFF0000u);
+    quad_pair_rows<BITS>(bf, (c & 1) != 0);  // in place: the buffer is refilled after the item
     Raw<BITS> rg[4];
     quad_groups<BITS>(bf, rg);
 #pragma unroll
