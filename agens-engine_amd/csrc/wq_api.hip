@@ -98,6 +98,17 @@ Segs make_segs(int nseg, const void* const* wt, const void* const* st, void* con
   return g;
 }
 
+// Two tokens on the wide linears go to the tokens-in-A-rows kernel (one MFMA row group holds both tokens) instead of
+// the line-load kernel (one token pass per token): measured at 2 tokens, gate_up W2 55296 x 5120 25.0 -> 18.6 us, the
+// LM head W4 152064 x 5120 71.5 -> 67.2 us; gate_up W3 / W4 even (27.4 / 27.7 against 27.7 / 28.4), and the
+// narrow QKV, O and down slower there (10.5 -> 13.0, 8.8 -> 12.0, 18.3 -> 22.1 us).  The same bits either way.
+bool two_tokens_on_mt(int bits, int m, const Segs& g) {
+  if (m != 2) return false;
+  long long rows = 0;
+  for (int i = 0; i < g.nseg; ++i) rows += g.n[i];
+  return rows >= 100000 || (bits == 2 && rows >= 32768);
+}
+
 // the default path for m <= 16 tokens: 9..16 tokens in one launch of the tokens-in-A-rows kernel where it takes them,
 // else in launches of at most 8: one or two tokens on the line-load kernel
 // (wq_i8m1d.hip) when their activations fit the LDS (measured faster there), otherwise and for 3..8 tokens the
@@ -117,7 +128,7 @@ int run_i8(int bits, const void* x, int m, const Segs& g, int k, int group, hipS
     Segs gg = g;
     for (int i = 0; i < g.nseg; ++i) gg.y[i] = g.y[i] + (size_t)m0 * g.ldy[i];
     const void* xx = static_cast<const uint16_t*>(x) + (size_t)m0 * xk;
-    int e = mm <= 2 ? i8_gemv_m1(bits, xx, mm, gg, k, group, s, act) : AK_INVALID;
+    int e = mm <= 2 && !two_tokens_on_mt(bits, mm, g) ? i8_gemv_m1(bits, xx, mm, gg, k, group, s, act) : AK_INVALID;
     if (e == AK_INVALID) e = i8_gemv_mt(bits, xx, mm, gg, k, group, s, act);
     if (e == AK_INVALID) e = i8_gemv_m1(bits, xx, mm, gg, k, group, s, act);
     if (e == AK_INVALID && m0 == 0) {

@@ -114,7 +114,7 @@ def assert_oracle(y, L, bits, x, m, what):
 
 
 @pytest.mark.parametrize("bits,n,k,m", [(3, 55296, 5120, 16), (2, 5120, 27648, 16), (4, 7168, 5120, 40),
-                                        (3, 5120, 5120, 128), (2, 1000, 2048, 9)])
+                                        (3, 5120, 5120, 128), (2, 1000, 2048, 9), (2, 55296, 5120, 2)])
 def test_default_route_against_oracle(bits, n, k, m):
     L = lin(7400 + bits + m, n, k, bits, 128)
     x = gen_x(7401 + m, m * k, 0.5 if k > 8192 else 1.0)
@@ -162,3 +162,20 @@ def test_conveniences_default_route():
         check(K.ak_w4_mma_gemv(X.p, L4.wt.p, L4.st.p, Y.p, m, 700, k, 128, None), "w4 mma")
         check(K.ak_synchronize())
         assert_oracle(Y.get(np.uint16, m * 700).reshape(m, 700), L4, 4, x, m, f"w4 mma m={m}")
+
+
+@pytest.mark.parametrize("bits", [2, 3])
+def test_two_tokens_on_wide_linears_equal_single_token(bits):
+    """Two tokens on a wide linear (gate_up 55296 x 5120; W2 takes the tokens-in-A-rows kernel there, W3 the line-load
+    kernel): each token's row bit-identical to its one-token launch (kernels/bench/test_w4.cu:143-158)."""
+    K = kernels()
+    n, k = 55296, 5120
+    L = lin(7700 + bits, n, k, bits, 128)
+    x = gen_x(7710 + bits, 2 * k)
+    X, Y2, Y1 = Dev.of(x), Dev(2 * n * 2), Dev(2 * n * 2)
+    multi(bits, X, 2, L, Y2, k, 128)
+    for t in range(2):
+        multi(bits, X, 1, L, Y1, k, 128, x_off=t * k * 2, y_off=t * n * 2)
+    check(K.ak_synchronize())
+    a, b = Y2.get(np.uint16, 2 * n), Y1.get(np.uint16, 2 * n)
+    assert np.array_equal(a, b), f"W{bits}: {int(np.sum(a != b))} outputs of the 2-token launch differ"
