@@ -878,7 +878,7 @@ int launch_m1d(I8Args a, hipStream_t s) {
 }
 
 // ---- chained launches: one persistent workgroup per CU runs the steps in order
-constexpr int kSplitK = 256, kAct = 512;
+constexpr int kSplitK = 256, kAct = 512, kChainLean = 16;
 struct ChainStep {
   I8Args a;
   int kind;  // bits * 16 + SPLIT, + kSplitK for a split-K step, + kAct for a split-K step with SiLU(gate) * up
@@ -889,7 +889,9 @@ struct ChainStep {
 // epochs: one word per workgroup in the chain's memory, the number of launches of this chain so far (every workgroup
 // counts every launch, so they agree); the tag of a launch is the low 16 bits of its epoch + 1, which differ from the
 // tags the previous launch left in the tagged copies and from their initial zeros
-template <int MT>
+// LEAN: only the step kinds of one- or two-stripe-set steps and plain split-K steps (the decode sweep's): a smaller
+// kernel (the chained kernel is sensitive to its code size: the M = 1 sweep 2921-2925 -> 2913-2918 us on one box)
+template <int MT, bool LEAN>
 __global__ void __launch_bounds__(1024, 1) i8_chain_kernel(const ChainStep* __restrict__ steps, int nsteps,
                                                            uint32_t* __restrict__ epochs) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -903,25 +905,39 @@ __global__ void __launch_bounds__(1024, 1) i8_chain_kernel(const ChainStep* __re
     const ChainStep st = steps[s];  // a copy: the step's fields live in scalar registers
     const bool w = st.wait != 0;
     const uint32_t target = f0 + (uint32_t)s;
-    switch (st.kind) {
-      case 4 * 16 + 1: m1d_body<4, 1, D, MT, true>(st.a, lds, w, target, tag); break;
-      case 4 * 16 + 2: m1d_body<4, 2, D, MT, true>(st.a, lds, w, target, tag); break;
-      case 4 * 16 + 4: m1d_body<4, 4, D, MT, true>(st.a, lds, w, target, tag); break;
-      case 4 * 16 + 8: m1d_body<4, 8, D, MT, true>(st.a, lds, w, target, tag); break;
-      case 3 * 16 + 1: m1d_body<3, 1, D, MT, true>(st.a, lds, w, target, tag); break;
-      case 3 * 16 + 2: m1d_body<3, 2, D, MT, true>(st.a, lds, w, target, tag); break;
-      case 3 * 16 + 4: m1d_body<3, 4, D, MT, true>(st.a, lds, w, target, tag); break;
-      case 3 * 16 + 8: m1d_body<3, 8, D, MT, true>(st.a, lds, w, target, tag); break;
-      case 2 * 16 + 1: m1d_body<2, 1, D, MT, true>(st.a, lds, w, target, tag); break;
-      case 2 * 16 + 2: m1d_body<2, 2, D, MT, true>(st.a, lds, w, target, tag); break;
-      case 2 * 16 + 4: m1d_body<2, 4, D, MT, true>(st.a, lds, w, target, tag); break;
-      case kSplitK + 4 * 16 + 1: m1d_body<4, 1, D, MT, true, true>(st.a, lds, w, target, tag); break;
-      case kSplitK + 3 * 16 + 1: m1d_body<3, 1, D, MT, true, true>(st.a, lds, w, target, tag); break;
-      case kSplitK + 2 * 16 + 1: m1d_body<2, 1, D, MT, true, true>(st.a, lds, w, target, tag); break;
-      case kAct + kSplitK + 4 * 16 + 1: m1d_body<4, 1, D, MT, true, true, true>(st.a, lds, w, target, tag); break;
-      case kAct + kSplitK + 3 * 16 + 1: m1d_body<3, 1, D, MT, true, true, true>(st.a, lds, w, target, tag); break;
-      case kAct + kSplitK + 2 * 16 + 1: m1d_body<2, 1, D, MT, true, true, true>(st.a, lds, w, target, tag); break;
-      default: m1d_body<2, 8, D, MT, true>(st.a, lds, w, target, tag); break;
+    if constexpr (LEAN) {
+      switch (st.kind) {
+        case 4 * 16 + 1: m1d_body<4, 1, D, MT, true>(st.a, lds, w, target, tag); break;
+        case 4 * 16 + 2: m1d_body<4, 2, D, MT, true>(st.a, lds, w, target, tag); break;
+        case 3 * 16 + 1: m1d_body<3, 1, D, MT, true>(st.a, lds, w, target, tag); break;
+        case 3 * 16 + 2: m1d_body<3, 2, D, MT, true>(st.a, lds, w, target, tag); break;
+        case 2 * 16 + 2: m1d_body<2, 2, D, MT, true>(st.a, lds, w, target, tag); break;
+        case kSplitK + 4 * 16 + 1: m1d_body<4, 1, D, MT, true, true>(st.a, lds, w, target, tag); break;
+        case kSplitK + 3 * 16 + 1: m1d_body<3, 1, D, MT, true, true>(st.a, lds, w, target, tag); break;
+        case kSplitK + 2 * 16 + 1: m1d_body<2, 1, D, MT, true, true>(st.a, lds, w, target, tag); break;
+        default: m1d_body<2, 1, D, MT, true>(st.a, lds, w, target, tag); break;
+      }
+    } else {
+      switch (st.kind) {
+        case 4 * 16 + 1: m1d_body<4, 1, D, MT, true>(st.a, lds, w, target, tag); break;
+        case 4 * 16 + 2: m1d_body<4, 2, D, MT, true>(st.a, lds, w, target, tag); break;
+        case 4 * 16 + 4: m1d_body<4, 4, D, MT, true>(st.a, lds, w, target, tag); break;
+        case 4 * 16 + 8: m1d_body<4, 8, D, MT, true>(st.a, lds, w, target, tag); break;
+        case 3 * 16 + 1: m1d_body<3, 1, D, MT, true>(st.a, lds, w, target, tag); break;
+        case 3 * 16 + 2: m1d_body<3, 2, D, MT, true>(st.a, lds, w, target, tag); break;
+        case 3 * 16 + 4: m1d_body<3, 4, D, MT, true>(st.a, lds, w, target, tag); break;
+        case 3 * 16 + 8: m1d_body<3, 8, D, MT, true>(st.a, lds, w, target, tag); break;
+        case 2 * 16 + 1: m1d_body<2, 1, D, MT, true>(st.a, lds, w, target, tag); break;
+        case 2 * 16 + 2: m1d_body<2, 2, D, MT, true>(st.a, lds, w, target, tag); break;
+        case 2 * 16 + 4: m1d_body<2, 4, D, MT, true>(st.a, lds, w, target, tag); break;
+        case kSplitK + 4 * 16 + 1: m1d_body<4, 1, D, MT, true, true>(st.a, lds, w, target, tag); break;
+        case kSplitK + 3 * 16 + 1: m1d_body<3, 1, D, MT, true, true>(st.a, lds, w, target, tag); break;
+        case kSplitK + 2 * 16 + 1: m1d_body<2, 1, D, MT, true, true>(st.a, lds, w, target, tag); break;
+        case kAct + kSplitK + 4 * 16 + 1: m1d_body<4, 1, D, MT, true, true, true>(st.a, lds, w, target, tag); break;
+        case kAct + kSplitK + 3 * 16 + 1: m1d_body<3, 1, D, MT, true, true, true>(st.a, lds, w, target, tag); break;
+        case kAct + kSplitK + 2 * 16 + 1: m1d_body<2, 1, D, MT, true, true, true>(st.a, lds, w, target, tag); break;
+        default: m1d_body<2, 8, D, MT, true>(st.a, lds, w, target, tag); break;
+      }
     }
     // signal: this workgroup's outputs of steps <= s are stored (each wave waits for its own stores' acknowledgement,
     // which for sc1 stores means written through to device scope).  Without a signal the workgroup goes on at once
@@ -1062,6 +1078,11 @@ int m1d_chain_make(int nsteps, const int* bits, const void* const* x, const int*
       h[i].a.part = reinterpret_cast<float*>(static_cast<uint8_t*>(d) + zoff[(size_t)i] + 4096);
     }
   }
+  bool lean = true;  // every step a kind of the lean kernel
+  for (int i = 0; i < nsteps; ++i) {
+    const int kd = h[i].kind, sp = kd & 15;
+    lean = lean && (kd < kSplitK ? sp == 1 || sp == 2 : kd < kAct && sp == 1);
+  }
   if (!e) e = (int)hipMemcpy(d, h, (size_t)nsteps * sizeof(ChainStep), hipMemcpyHostToDevice);
   free(h);
   if (e) {
@@ -1069,7 +1090,7 @@ int m1d_chain_make(int nsteps, const int* bits, const void* const* x, const int*
     return e == (int)hipErrorOutOfMemory ? AK_OOM : e;
   }
   *table = d;
-  *mt_out = mt;
+  *mt_out = mt + (lean ? kChainLean : 0);
   *smem_out = smem;
   return 0;
 }
@@ -1078,10 +1099,16 @@ int m1d_chain_launch(const void* table, int nsteps, int mt, size_t smem, hipStre
   const ChainStep* t = static_cast<const ChainStep*>(table);
   uint32_t* ep = reinterpret_cast<uint32_t*>(const_cast<uint8_t*>(static_cast<const uint8_t*>(table)) +
                                              (((size_t)nsteps * sizeof(ChainStep) + 255) & ~(size_t)255));
-  if (mt == 1)
-    hipLaunchKernelGGL(i8_chain_kernel<1>, dim3(num_cus()), dim3(1024), smem, s, t, nsteps, ep);
-  else
-    hipLaunchKernelGGL(i8_chain_kernel<2>, dim3(num_cus()), dim3(1024), smem, s, t, nsteps, ep);
+  switch (mt) {  // + kChainLean: every step has a kind of the lean kernel
+    case 1: hipLaunchKernelGGL((i8_chain_kernel<1, false>), dim3(num_cus()), dim3(1024), smem, s, t, nsteps, ep); break;
+    case 2: hipLaunchKernelGGL((i8_chain_kernel<2, false>), dim3(num_cus()), dim3(1024), smem, s, t, nsteps, ep); break;
+    case 1 + kChainLean:
+      hipLaunchKernelGGL((i8_chain_kernel<1, true>), dim3(num_cus()), dim3(1024), smem, s, t, nsteps, ep);
+      break;
+    default:
+      hipLaunchKernelGGL((i8_chain_kernel<2, true>), dim3(num_cus()), dim3(1024), smem, s, t, nsteps, ep);
+      break;
+  }
   return (int)hipGetLastError();
 }
 
