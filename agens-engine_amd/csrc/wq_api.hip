@@ -27,6 +27,10 @@ int mm_gemv(int bits, const void* x, int m, const Segs& g, int k, int group, hip
 int m1d_chain_make(int nsteps, const int* bits, const void* const* x, const int* m, const int* k, const Segs* segs,
                    const int* wait, const int* act, void** table, int* mt_out, size_t* smem_out);
 int m1d_chain_launch(const void* table, int nsteps, int mt, size_t smem, hipStream_t s);
+int mt_chain_make(int nsteps, const int* bits, const void* const* x, const int* m, const int* k, const Segs* segs,
+                  const int* wait, void** table, int* nt_out, size_t* smem_out);
+int mt_chain_launch(const void* table, int nsteps, int nt, size_t smem, hipStream_t s);
+int mt_chain_error(int* err);
 int m1d_chain_error(int* err);
 void m1d_tune_override(int split, int nwv, int sk);
 int m1d_tune_query(int bits, int m, const Segs& g, int k, int* split, int* nwv, int* sk);
@@ -171,6 +175,7 @@ int gemv(int bits, const void* x, int m, int nseg, const void* const* wt, const 
 // one launch each.
 struct Chain {
   int nsteps = 0, mt = 1;
+  int kind = 0;  // 1: the one- and two-token chained kernel (wq_i8m1d.hip), 2: the 1..8-token one (wq_i8mt.hip)
   size_t smem = 0;
   void* table = nullptr;
   ak_wq_step* steps = nullptr;
@@ -416,11 +421,16 @@ int ak_wq_chain_create(const ak_wq_step* steps, int nsteps, void** chain) {
     return AK_OOM;
   }
   memcpy(c->steps, steps, sizeof(ak_wq_step) * (size_t)nsteps);
-  // the chained kernel takes default-numerics steps of group 128 and at most two tokens (the same bits as one launch
-  // per step); any other chain runs one launch per step
-  bool chainable = !exact_mode();
-  for (int i = 0; i < nsteps && chainable; ++i)
-    chainable = steps[i].bf16w == 0 && steps[i].group == 128 && steps[i].m <= 2;
+  // the chained kernels take default-numerics steps of group 128 (the same bits as one launch per step): at most two
+  // tokens the one-token kernel's steps, up to 4 tokens (no SiLU(gate) * up step) the tokens-in-A-rows kernel's; any
+  // other chain runs one launch per step
+  bool chainable = !exact_mode(), small = true, act_any = false;
+  for (int i = 0; i < nsteps && chainable; ++i) {
+    chainable = steps[i].bf16w == 0 && steps[i].group == 128 && steps[i].m <= 4;
+    small = small && steps[i].m <= 2;
+    act_any = act_any || steps[i].act;
+  }
+  if (chainable && !small && act_any) chainable = false;
   if (chainable) {
     int* ib = static_cast<int*>(malloc(sizeof(int) * 5 * (size_t)nsteps));
     const void** xs = static_cast<const void**>(malloc(sizeof(void*) * (size_t)nsteps));
@@ -435,7 +445,9 @@ int ak_wq_chain_create(const ak_wq_step* steps, int nsteps, void** chain) {
         bits[i] = st.bits, m[i] = st.m, k[i] = st.k, wait[i] = !st.independent, xs[i] = st.x, act[i] = st.act;
         sg[i] = make_segs(st.nseg, st.wt, st.st, st.y, st.n, ldy, 16);
       }
-      e = m1d_chain_make(nsteps, bits, xs, m, k, sg, wait, act, &c->table, &c->mt, &c->smem);
+      e = small ? m1d_chain_make(nsteps, bits, xs, m, k, sg, wait, act, &c->table, &c->mt, &c->smem)
+                : mt_chain_make(nsteps, bits, xs, m, k, sg, wait, &c->table, &c->mt, &c->smem);
+      c->kind = e ? 0 : small ? 1 : 2;
     }
     free(ib);
     free(xs);
@@ -457,7 +469,8 @@ int ak_wq_chain_run(void* chain, void* stream) {
   if (c->table) {
     ChainGuard g;
     if (const int e = g.begin(s)) return e;
-    const int e = m1d_chain_launch(c->table, c->nsteps, c->mt, c->smem, s);
+    const int e = c->kind == 1 ? m1d_chain_launch(c->table, c->nsteps, c->mt, c->smem, s)
+                               : mt_chain_launch(c->table, c->nsteps, c->mt, c->smem, s);
     return e ? e : g.end(s);
   }
   for (int i = 0; i < c->nsteps; ++i)
@@ -477,9 +490,10 @@ int ak_wq_chain_destroy(void* chain) {
 }
 
 int ak_wq_chain_status(void) {
-  int err = 0;
-  const int e = m1d_chain_error(&err);
-  return e ? -e : err;
+  int err = 0, err2 = 0;
+  int e = m1d_chain_error(&err);
+  if (!e) e = mt_chain_error(&err2);
+  return e ? -e : (err || err2 ? 1 : 0);
 }
 
 int ak_wq_tune_override(int split, int nwv, int sk) {

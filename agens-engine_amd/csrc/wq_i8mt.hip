@@ -32,6 +32,10 @@
 #include "wq_i8_common.h"
 #include "wq_quad.h"
 
+#include <stdlib.h>
+
+#include <vector>
+
 namespace agq {
 
 int num_cus();
@@ -43,6 +47,48 @@ constexpr int kG = 128;
 constexpr int kRsrcWord3 = 0x00020000;  // raw buffer resource, dword 3 (CDNA)
 constexpr int kNt = 2;                    // streaming (non-temporal) cache policy for the weights
 constexpr int kVmcnt0 = 0x0F70;            // s_waitcnt immediate: vector memory counter 0, the others unconstrained
+constexpr int kSc1 = 16;                  // device-scope coherent access (sc1): misses / writes through the L2
+
+// Chained launches of this kernel's steps (3..4 tokens): one persistent workgroup per CU runs the steps in order.  A
+// step that reads earlier steps' outputs either waits at a grid barrier (every workgroup's flag word reaches the
+// step) or, where its activations are the output of the step just before it, polls a tagged copy of that output
+// (32-bit words bf16 | tag << 16, the tag the low 16 bits of the launch count + 1) until every word it reads carries
+// the launch's tag.  Outputs are written with device-coherent stores; the steps' own LDS is reused after an LDS-only
+// barrier.  Waits are bounded (0.2 s of the wall clock; then the error flag is raised and the step goes on).
+constexpr int kMtChainMaxWg = 1024;
+constexpr long long kMtChainSpinTicks = 20000000;  // 0.2 s of the 100 MHz wall clock
+constexpr uint32_t kMtTagMask = 0xFFFFu;
+__device__ __attribute__((aligned(256))) uint32_t g_mt_chain_flags[kMtChainMaxWg];
+__device__ uint32_t g_mt_chain_err;
+
+// wave 0 polls until the flags of workgroups [0, nwg) are all at least `target` (wrap-safe), 16 bytes per lane
+__device__ __forceinline__ void mt_chain_poll(uint32_t target) {
+  const int lane = threadIdx.x, nwg = gridDim.x;
+  const long long t0 = wall_clock64();
+  const __amdgpu_buffer_rsrc_t rf =
+      __builtin_amdgcn_make_buffer_rsrc(g_mt_chain_flags, (short)0, kMtChainMaxWg * 4, kRsrcWord3);
+  for (;;) {
+    bool ok = true;
+    for (int j = 4 * lane; j < nwg; j += 256) {
+      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rf, j * 4, 0, kSc1);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ok = ok && (j + i >= nwg || (int)(v[i] - target) >= 0);
+    }
+    if (__all(ok)) break;
+    if (wall_clock64() - t0 > kMtChainSpinTicks) {
+      if (lane == 0) __hip_atomic_store(&g_mt_chain_err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+// the workgroup meets at an LDS-only barrier (loads in flight stay in flight)
+__device__ __forceinline__ void mt_lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
 
 // LDS bytes of the activation image (per group: 2 halves x NT token groups x 4 chunks x 192 B) and its meta
 __host__ __device__ inline int mt_a_bytes(int ngroups, int nt) { return ngroups * 2 * nt * 768; }
@@ -60,12 +106,17 @@ __host__ __device__ inline int mt_meta_bytes(int ngroups, int nt) { return nt * 
 // TH (split-K only, one segment, 9..16 tokens as NT = 2): the launch holds two token halves, workgroups [0, W) for
 // tokens 0..7 and [W, 2W) for tokens 8.. (W = a.wg_end[3]); each half computes exactly what the 8-token launch of its
 // tokens computes, with its own stripe partials and counters.
-template <int BITS, int SPLIT, int DEPTH, int NT, bool CH, bool SK = false, bool ACT = false, bool TH = false>
-__global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
+// CHAIN (whole-image and split-K steps, no SiLU(gate) * up): a step of a chained launch (see mt_chain_poll): workgroups
+// past the step's grid return at once (after the step's wait); the activations are requested after the step's first
+// weights and its wait, device-coherently or from the tagged copy a.xtg; outputs are stored device-coherently, with
+// their tagged copy where a.ytg asks for it.
+template <int BITS, int SPLIT, int DEPTH, int NT, bool CH, bool SK = false, bool ACT = false, bool TH = false,
+          bool CHAIN = false>
+__device__ __forceinline__ void mt_body(const I8Args& a, uint8_t* lds, bool wait, uint32_t target, uint32_t tag) {
   static_assert(!TH || (SK && NT == 2), "token halves: split-K launches of 8-token halves");
   static_assert((!CH && !SK) || SPLIT == 1, "chunked and split launches give every wave whole stripes of its blocks");
   static_assert(!(CH && SK), "one of the two");
-  extern __shared__ __attribute__((aligned(256))) uint8_t lds[];
+  static_assert(!CHAIN || (!CH && !TH && !ACT), "chained steps: whole-image or split-K launches");
   constexpr int LPU = kG / 8, UPW = 64 / LPU, XB = 4, MP = 4 * NT;  // MP: padded tokens
   constexpr int REC = 128 * BITS;
   const int P = a.P, nquad = a.nquad, k = a.k;
@@ -78,6 +129,12 @@ __global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const Segs& sgs = a.segs;
+  if constexpr (CHAIN) {
+    if ((int)blockIdx.x >= AK_PICK(sgs.nseg - 1, a.wg_end)) {  // no rows in this step
+      if (wait && wave == 0) mt_chain_poll(target);
+      return;
+    }
+  }
 
   // this workgroup's segment and its 16-row blocks [b_lo, b_lo + nb) of that segment (SK: row range r, stripe psk)
   int sg = 0;
@@ -147,6 +204,54 @@ __global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
   const int u0 = wave * UPW + lane / LPU;
   const int npass = (units + ustride - 1) / ustride;
   uint4 xv[XB];
+  // chained: x (the step's activations, mm x k) read device-coherently, or its tagged copy a.xtg (the same layout in
+  // 32-bit words) polled until every word the wave holds carries the launch's tag
+  const __amdgpu_buffer_rsrc_t rx =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(xb), (short)0, mm * k * 2, kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rxt =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(a.xtg), (short)0, mm * k * 4, kRsrcWord3);
+  const bool tagged = CHAIN && a.xtg != nullptr;
+  const uint32_t tag2 = (tag & kMtTagMask) * 0x10001u;
+  (void)rx, (void)rxt, (void)tag2;
+  auto ld_coherent = [&](int o) __attribute__((always_inline)) {
+    if constexpr (BITS == 4) {
+      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rx, (o + unit_pair_offset<4>(sub, 0)) * 2, 0, kSc1);
+      return make_uint4(v[0], v[1], v[2], v[3]);
+    } else {
+      uint32_t v[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        v[q] = __builtin_amdgcn_raw_buffer_load_b32(rx, (o + unit_pair_offset<BITS>(sub, q)) * 2, 0, kSc1);
+      return make_uint4(v[0], v[1], v[2], v[3]);
+    }
+  };
+  // the lane's pairs of the unit at element offset o from the tagged copy (device-coherent): whether all carry the tag
+  auto ld_tagged = [&](int o, uint4& v) __attribute__((always_inline)) {
+    typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+    uint32_t lo[4], hi[4];
+    if constexpr (BITS == 4) {
+      const int bo = (o + unit_pair_offset<4>(sub, 0)) * 4;
+      const u32x4 d0 = __builtin_amdgcn_raw_buffer_load_b128(rxt, bo, 0, kSc1);
+      const u32x4 d1 = __builtin_amdgcn_raw_buffer_load_b128(rxt, bo + 16, 0, kSc1);
+      lo[0] = d0[0], hi[0] = d0[1], lo[1] = d0[2], hi[1] = d0[3];
+      lo[2] = d1[0], hi[2] = d1[1], lo[3] = d1[2], hi[3] = d1[3];
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const u32x2 d = __builtin_amdgcn_raw_buffer_load_b64(rxt, (o + unit_pair_offset<BITS>(sub, q)) * 4, 0, kSc1);
+        lo[q] = d[0], hi[q] = d[1];
+      }
+    }
+    bool ok = true;
+    uint32_t w[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      w[q] = __builtin_amdgcn_perm(hi[q], lo[q], 0x05040100u);              // the two values
+      ok = ok && __builtin_amdgcn_perm(hi[q], lo[q], 0x07060302u) == tag2;  // the two tags
+    }
+    v = make_uint4(w[0], w[1], w[2], w[3]);
+    return ok;
+  };
   auto xload = [&](int pass0) {
 #pragma unroll
     for (int b = 0; b < XB; ++b) {
@@ -155,15 +260,40 @@ __global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
       xv[b] = make_uint4(0u, 0u, 0u, 0u);
       if (pass0 + b < npass) {
         const size_t xo = ok ? (size_t)t * (ACT ? 2 * k : k) + gk : 0;  // the unit's group
-        uint4 v = load_unit<BITS>(xb + xo, sub);
-        if constexpr (ACT) v = silu_mul8(v, load_unit<BITS>(xb + xo + k, sub));
-        xv[b] = ok ? v : make_uint4(0u, 0u, 0u, 0u);
+        if constexpr (CHAIN) {
+          if (tagged) {
+            if (wave * UPW + (pass0 + b) * ustride >= units) continue;  // no unit of this wave in the pass (uniform)
+            const long long t0 = wall_clock64();
+            for (;;) {
+              uint4 v;
+              const bool got = ld_tagged((int)xo, v);
+              if (__all(got || !ok)) {
+                xv[b] = ok ? v : make_uint4(0u, 0u, 0u, 0u);
+                break;
+              }
+              if (wall_clock64() - t0 > kMtChainSpinTicks) {
+                if (lane == 0) __hip_atomic_store(&g_mt_chain_err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+              }
+              __builtin_amdgcn_s_sleep(1);
+            }
+          } else {
+            const uint4 v = ld_coherent((int)xo);
+            xv[b] = ok ? v : make_uint4(0u, 0u, 0u, 0u);
+          }
+        } else {
+          uint4 v = load_unit<BITS>(xb + xo, sub);
+          if constexpr (ACT) v = silu_mul8(v, load_unit<BITS>(xb + xo + k, sub));
+          xv[b] = ok ? v : make_uint4(0u, 0u, 0u, 0u);
+        }
       }
     }
   };
-  xload(0);
+  if constexpr (!CHAIN) {
+    xload(0);
 #pragma unroll
-  for (int b = 0; b < XB; ++b) asm volatile("" ::"v"(xv[b].x), "v"(xv[b].y), "v"(xv[b].z), "v"(xv[b].w));
+    for (int b = 0; b < XB; ++b) asm volatile("" ::"v"(xv[b].x), "v"(xv[b].y), "v"(xv[b].z), "v"(xv[b].w));
+  }
 
   // ---- this wave's tasks: stripe set j, quads [qa, qb), blocks b0w, b0w + bstep, ... < nb
   const int j = wave % SPLIT, bstep = nwv / SPLIT, b0w = wave / SPLIT;
@@ -229,6 +359,11 @@ __global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
   };
 #pragma unroll
   for (int d = 0; d < DEPTH; ++d) fetch_next(buf[d]);
+  if constexpr (CHAIN) {  // the first weights are requested: now the wait and the activations
+    if (wait && wave == 0) mt_chain_poll(target);
+    if (wait) mt_lds_barrier();
+    xload(0);
+  }
 
   // ---- activations, step 2: limbs into the A image, bias sums and activation scale into meta
   auto convert = [&](int p0) {
@@ -423,10 +558,26 @@ __global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
     }
   }
   __syncthreads();
+  uint32_t* const ytg = CHAIN ? AK_PICK(sg, a.ytg) : nullptr;
   for (int i = tid; i < nb * MP * 16; i += 64 * nwv) {
     const int bl = i / (MP * 16), t = (i / 16) % MP, row = (b_lo + bl) * 16 + (i & 15);
-    if (t < mm && row < n) yseg[(size_t)t * ldy + row] = yl[i];
+    if (t < mm && row < n) {
+      if constexpr (CHAIN) {
+        __hip_atomic_store(yseg + (size_t)t * ldy + row, yl[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (ytg)
+          __hip_atomic_store(ytg + (size_t)t * ldy + row, (uint32_t)yl[i] | ((tag & kMtTagMask) << 16),
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      } else {
+        yseg[(size_t)t * ldy + row] = yl[i];
+      }
+    }
   }
+}
+
+template <int BITS, int SPLIT, int DEPTH, int NT, bool CH, bool SK = false, bool ACT = false, bool TH = false>
+__global__ void __launch_bounds__(1024, 1) i8_mt_kernel(const I8Args a) {
+  extern __shared__ __attribute__((aligned(256))) uint8_t lds[];
+  mt_body<BITS, SPLIT, DEPTH, NT, CH, SK, ACT, TH>(a, lds, false, 0u, 0u);
 }
 
 size_t mt_block_bytes(int P, int split, int nt) {  // per 16-row block: outputs, partials, ticket
@@ -583,6 +734,134 @@ int launch_mt(I8Args a, hipStream_t s) {
   return AK_INVALID;
 }
 
+// ---- chained launches (3..4 tokens)
+constexpr int kMtSplitK = 256;
+struct MtChainStep {
+  I8Args a;
+  int kind;    // bits * 16 + SPLIT (whole activation image), + kMtSplitK for a split-K step (SPLIT 1)
+  int wait;    // 1: the step reads (or overwrites) what earlier steps wrote or read: the grid barrier
+  int signal;  // 1: a later step waits at the grid barrier for this one: the flags move after it
+};
+
+// epochs: one word per workgroup, the launches of this chain so far (the tag of a launch: the low 16 bits of its
+// epoch + 1, which differ from the previous launch's tags and from the initial zeros)
+template <int NT>
+__global__ void __launch_bounds__(1024, 1) i8_mt_chain_kernel(const MtChainStep* __restrict__ steps, int nsteps,
+                                                              uint32_t* __restrict__ epochs) {
+  extern __shared__ __attribute__((aligned(256))) uint8_t lds[];
+  constexpr int D = NT > 2 ? 1 : 2;
+  uint32_t* const flag = g_mt_chain_flags + blockIdx.x;
+  // every workgroup's flag holds the same count between chained launches (all of them signal the last step)
+  const uint32_t f0 =
+      __builtin_amdgcn_readfirstlane(__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  const uint32_t ep = __builtin_amdgcn_readfirstlane(epochs[blockIdx.x]);
+  const uint32_t tag = (ep + 1u) & kMtTagMask;
+  for (int s = 0; s < nsteps; ++s) {
+    const MtChainStep st = steps[s];
+    const bool w = st.wait != 0;
+    const uint32_t target = f0 + (uint32_t)s;
+    switch (st.kind) {
+      case 4 * 16 + 1: mt_body<4, 1, D, NT, false, false, false, false, true>(st.a, lds, w, target, tag); break;
+      case 4 * 16 + 2: mt_body<4, 2, D, NT, false, false, false, false, true>(st.a, lds, w, target, tag); break;
+      case 4 * 16 + 4: mt_body<4, 4, D, NT, false, false, false, false, true>(st.a, lds, w, target, tag); break;
+      case 4 * 16 + 8: mt_body<4, 8, D, NT, false, false, false, false, true>(st.a, lds, w, target, tag); break;
+      case 3 * 16 + 1: mt_body<3, 1, D, NT, false, false, false, false, true>(st.a, lds, w, target, tag); break;
+      case 3 * 16 + 2: mt_body<3, 2, D, NT, false, false, false, false, true>(st.a, lds, w, target, tag); break;
+      case 3 * 16 + 4: mt_body<3, 4, D, NT, false, false, false, false, true>(st.a, lds, w, target, tag); break;
+      case 3 * 16 + 8: mt_body<3, 8, D, NT, false, false, false, false, true>(st.a, lds, w, target, tag); break;
+      case 2 * 16 + 2: mt_body<2, 2, D, NT, false, false, false, false, true>(st.a, lds, w, target, tag); break;
+      case 2 * 16 + 4: mt_body<2, 4, D, NT, false, false, false, false, true>(st.a, lds, w, target, tag); break;
+      case 2 * 16 + 8: mt_body<2, 8, D, NT, false, false, false, false, true>(st.a, lds, w, target, tag); break;
+      case kMtSplitK + 4 * 16 + 1: mt_body<4, 1, D, NT, false, true, false, false, true>(st.a, lds, w, target, tag); break;
+      case kMtSplitK + 3 * 16 + 1: mt_body<3, 1, D, NT, false, true, false, false, true>(st.a, lds, w, target, tag); break;
+      case kMtSplitK + 2 * 16 + 1: mt_body<2, 1, D, NT, false, true, false, false, true>(st.a, lds, w, target, tag); break;
+      default: mt_body<2, 1, D, NT, false, false, false, false, true>(st.a, lds, w, target, tag); break;  // W2, 1
+    }
+    // signal: this workgroup's outputs of steps <= s are stored (each wave waits for its stores' acknowledgement,
+    // which for device-coherent stores means written through); otherwise the workgroup goes on at once
+    if (st.signal || s + 1 == nsteps) {
+      __builtin_amdgcn_s_waitcnt(kVmcnt0);
+      __syncthreads();
+      if (threadIdx.x == 0) __hip_atomic_store(flag, f0 + (uint32_t)s + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+      mt_lds_barrier();
+    }
+  }
+  if (threadIdx.x == 0) epochs[blockIdx.x] = ep + 1u;
+}
+
+// The launch shape of one chained step (the choices of launch_mt without its chunked and token-halves forms): 0 with
+// a.wg_end, *kind, *smem and *scratch (bytes of counters and stripe partials, split-K only) set; AK_INVALID if the
+// step needs a form the chained kernel does not run.
+int mt_chain_plan(I8Args& a, int bits, int nt, int* kind, size_t* smem, size_t* scratch) {
+  const Segs& g = a.segs;
+  const int ngroups = a.nquad * 4, ntile = a.nquad / 2;
+  for (int i = 0; i < g.nseg; ++i)
+    if ((long long)ntile * g.n[i] * 128 * bits >= (1ll << 31)) return AK_INVALID;
+  int total = 0;
+  for (int i = 0; i < g.nseg; ++i) total += (g.n[i] + 15) / 16;
+  const int cus = num_cus();
+  int per = (total + cus - 1) / cus, grid = 0;
+  for (;; ++per) {
+    grid = 0;
+    for (int i = 0; i < g.nseg; ++i) grid += ((g.n[i] + 15) / 16 + per - 1) / per;
+    if (grid <= cus || per >= total) break;
+  }
+  if (grid > cus) return AK_INVALID;
+  for (int i = 0, e = 0; i < kMaxSegs; ++i) {
+    if (i < g.nseg) e += ((g.n[i] + 15) / 16 + per - 1) / per;
+    a.wg_end[i] = e;
+  }
+  int nbmax = 0;
+  for (int i = 0; i < g.nseg; ++i) {
+    const int nbs = (g.n[i] + 15) / 16, gs = (nbs + per - 1) / per;
+    nbmax = (nbs + gs - 1) / gs > nbmax ? (nbs + gs - 1) / gs : nbmax;
+  }
+  const size_t x_bytes = 256 + (size_t)mt_a_bytes(ngroups, nt) + mt_meta_bytes(ngroups, nt);
+  if (a.P >= 2 && (total <= 2 * cus || (x_bytes > 140 * 1024 && total <= AK_MT_SK_BLOCKS * cus))) {
+    const int nrt = cus / a.P;
+    int nr[kMaxSegs] = {0, 0, 0, 0}, left = nrt - g.nseg, nbr = 0;
+    size_t part_floats = 0;
+    for (int i = 0; i < g.nseg; ++i) {
+      const int nbs = (g.n[i] + 15) / 16;
+      nr[i] = 1 + (int)((long long)left * nbs / total);
+      nbr = (nbs + nr[i] - 1) / nr[i] > nbr ? (nbs + nr[i] - 1) / nr[i] : nbr;
+      part_floats += (size_t)a.P * 4 * nt * nbs * 16;
+    }
+    const int cg = mt_chunk_groups(a.nquad, a.P, a.P);
+    const size_t sm = 256 + (size_t)mt_a_bytes(cg, nt) + mt_meta_bytes(cg, nt) + (size_t)nbr * 4 * nt * 16 * 2 + 16;
+    if (nrt < g.nseg || nrt > 1024 || sm > 160 * 1024) return AK_INVALID;
+    for (int i = 0, e = 0; i < kMaxSegs; ++i) {
+      if (i < g.nseg) e += nr[i] * a.P;
+      a.wg_end[i] = e;
+    }
+    *kind = kMtSplitK + bits * 16 + 1;
+    *smem = sm;
+    *scratch = 4096 + part_floats * 4;
+    return 0;
+  }
+  if (x_bytes > 140 * 1024) return AK_INVALID;
+  int best_split = 0;
+  double best = 1e30;
+  for (int split : {1, 2, 4, 8}) {
+    if (split > a.P) break;
+    if (x_bytes + (size_t)nbmax * mt_block_bytes(a.P, split, nt) + 16 > 160 * 1024) continue;
+    int lmax = 0;
+    for (int j = 0; j < split; ++j) {
+      const int l = stripe_begin((j + 1) * a.P / split, a.nquad, a.P, 2) - stripe_begin(j * a.P / split, a.nquad, a.P, 2);
+      lmax = l > lmax ? l : lmax;
+    }
+    const int bstep = 16 / split;
+    const double cost = (double)((nbmax + bstep - 1) / bstep) * (lmax + 1.0);
+    if (cost < best - 1e-9) best = cost, best_split = split;
+  }
+  if (!best_split) return AK_INVALID;
+  *kind = bits * 16 + best_split;
+  *smem = x_bytes + (size_t)nbmax * mt_block_bytes(a.P, best_split, nt) + 16;
+  *scratch = 0;
+  return 0;
+}
+
 }  // namespace
 
 // 1..16 tokens (4, 8 or 16 in the kernel), 16-row blocks (the last one padded); activations beyond the LDS: split-K
@@ -619,6 +898,106 @@ int i8_gemv_mt(int bits, const void* x, int m, const Segs& g, int k, int group, 
     case 24: return launch_mt<2, 4>(a, s);
     default: return AK_INVALID;
   }
+}
+
+// A chain of 1..4-token steps (at least one above 2) as one launch of the tokens-in-A-rows kernel's steps: the table of
+// steps in device memory (then the workgroups' epochs, the tagged output copies and the split-K steps' counters and
+// partials), or AK_INVALID if a step does not suit the chained kernel (the caller runs one launch per step).  Tagged
+// waits as in the one-token chain: step i reads a tagged copy of segment j of step i - 1's outputs where that segment
+// holds all of its activations (x = its start, rows dense), step i - 1 waited for the step before it (or is the
+// first) and step i + 1 waits (or there is none).  *nt_out: the kernel's token groups (1).
+int mt_chain_make(int nsteps, const int* bits, const void* const* x, const int* m, const int* k, const Segs* segs,
+                  const int* wait, void** table, int* nt_out, size_t* smem_out) {
+  // up to 4 tokens (one token group): with two token groups the chained sweep measured slower than one launch per
+  // step (M = 8, 64 layers + LM head: 5684-6215 us against 5488-5508 us; the two-group step bodies spill or run one
+  // item in flight per wave in the chained kernel)
+  const int nt = 1;
+  for (int i = 0; i < nsteps; ++i)
+    if (m[i] < 1 || m[i] > 4 || bits[i] < 2 || bits[i] > 4) return AK_INVALID;
+  if (num_cus() > kMtChainMaxWg) return AK_INVALID;
+  std::vector<MtChainStep> h((size_t)nsteps);
+  const size_t table_bytes = ((size_t)nsteps * sizeof(MtChainStep) + 255) & ~(size_t)255;
+  size_t total = table_bytes + kMtChainMaxWg * 4, smem = 0;
+  std::vector<size_t> zoff((size_t)nsteps, 0), zbytes((size_t)nsteps, 0), toff((size_t)nsteps, 0);
+  std::vector<int> tseg((size_t)nsteps, -1);
+  const char* ev = getenv("AK_CHAIN_TAGS");
+  const bool tags_on = !(ev && atoi(ev) == 0);
+  for (int i = 1; i < nsteps && tags_on; ++i) {
+    if (!wait[i] || (i > 1 && !wait[i - 1]) || (i + 1 < nsteps && !wait[i + 1])) continue;
+    const Segs& p = segs[i - 1];
+    for (int j = 0; j < p.nseg; ++j)
+      if (p.y[j] == x[i] && p.ldy[j] == p.n[j] && (long long)m[i] * k[i] <= (long long)m[i - 1] * p.n[j]) {
+        tseg[(size_t)i] = j;
+        toff[(size_t)i] = total;
+        total += ((size_t)m[i - 1] * p.n[j] * 4 + 255) & ~(size_t)255;
+        break;
+      }
+  }
+  for (int i = 0; i < nsteps; ++i) {
+    I8Args& a = h[(size_t)i].a;
+    a.segs = segs[i];
+    a.x = static_cast<const uint16_t*>(x[i]);
+    a.m = m[i];
+    a.k = k[i];
+    a.nquad = kpad(k[i]) / kG / 4;
+    a.qpt = 2;
+    a.P = stripe_count(a.nquad, a.qpt);
+    a.nb = 0;
+    a.part = nullptr;
+    a.cnt = nullptr;
+    a.act = 0;
+    size_t sm = 0, zb = 0;
+    if (mt_chain_plan(a, bits[i], nt, &h[(size_t)i].kind, &sm, &zb)) return AK_INVALID;
+    h[(size_t)i].wait = i > 0 && wait[i] && tseg[(size_t)i] < 0 ? 1 : 0;
+    h[(size_t)i].signal = i + 1 < nsteps && wait[i + 1] && tseg[(size_t)i + 1] < 0 ? 1 : 0;
+    smem = sm > smem ? sm : smem;
+    if (zb) {
+      zoff[(size_t)i] = total;
+      zbytes[(size_t)i] = zb;
+      total += (zb + 255) & ~(size_t)255;
+    }
+  }
+  void* d = nullptr;
+  int e = (int)hipMalloc(&d, total);
+  if (!e) e = (int)hipMemset(static_cast<uint8_t*>(d) + table_bytes, 0, total - table_bytes);
+  for (int i = 0; i < nsteps && !e; ++i) {
+    if (tseg[(size_t)i] >= 0) {
+      uint32_t* tb = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(d) + toff[(size_t)i]);
+      h[(size_t)i].a.xtg = tb;
+      h[(size_t)i - 1].a.ytg[tseg[(size_t)i]] = tb;
+    }
+    if (zbytes[(size_t)i]) {
+      h[(size_t)i].a.cnt = reinterpret_cast<int*>(static_cast<uint8_t*>(d) + zoff[(size_t)i]);
+      h[(size_t)i].a.part = reinterpret_cast<float*>(static_cast<uint8_t*>(d) + zoff[(size_t)i] + 4096);
+    }
+  }
+  if (!e) e = (int)hipMemcpy(d, h.data(), (size_t)nsteps * sizeof(MtChainStep), hipMemcpyHostToDevice);
+  if (e) {
+    if (d) (void)hipFree(d);
+    return e == (int)hipErrorOutOfMemory ? AK_OOM : e;
+  }
+  *table = d;
+  *nt_out = nt;
+  *smem_out = smem;
+  return 0;
+}
+
+int mt_chain_launch(const void* table, int nsteps, int nt, size_t smem, hipStream_t s) {
+  const MtChainStep* t = static_cast<const MtChainStep*>(table);
+  uint32_t* ep = reinterpret_cast<uint32_t*>(const_cast<uint8_t*>(static_cast<const uint8_t*>(table)) +
+                                             (((size_t)nsteps * sizeof(MtChainStep) + 255) & ~(size_t)255));
+  if (nt != 1) return AK_INVALID;
+  hipLaunchKernelGGL(i8_mt_chain_kernel<1>, dim3(num_cus()), dim3(1024), smem, s, t, nsteps, ep);
+  return (int)hipGetLastError();
+}
+
+// reads and clears the flag a chained launch of these steps raises when a bounded wait ran out
+int mt_chain_error(int* err) {
+  uint32_t v = 0, z = 0;
+  int e = (int)hipMemcpyFromSymbol(&v, HIP_SYMBOL(g_mt_chain_err), sizeof(v), 0, hipMemcpyDeviceToHost);
+  if (!e && v) e = (int)hipMemcpyToSymbol(HIP_SYMBOL(g_mt_chain_err), &z, sizeof(z), 0, hipMemcpyHostToDevice);
+  *err = (int)v;
+  return e;
 }
 
 }  // namespace agq

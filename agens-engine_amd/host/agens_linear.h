@@ -113,8 +113,8 @@ class LinearChain {
   // ak_wq_chain_create over the steps: validates, allocates and uploads the step table (synchronous; not under stream
   // capture).  0 or an error code.
   int build();
-  // one launch on `stream` (one launch per step where the chained kernel does not take a step: group 64, more than two
-  // tokens, exact numerics); allocates nothing and can be captured.  hipErrorNotReady (600) while the device's last
+  // one launch on `stream` (one launch per step where the chained kernels do not take a step: group 64, more than four
+  // tokens, more than two with a fused activation step, exact numerics); allocates nothing and can be captured.  hipErrorNotReady (600) while the device's last
   // chained launch, issued on another stream, is still running (chained launches on one device share its flag words).
   int run(void* stream);
   // 1: runs as one chained launch, 0: as one launch per step (after build())

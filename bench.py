@@ -322,7 +322,8 @@ def run_sweep(args, K, B):
                 ctraffic = json.load(open(tf)).get("chain_sweep", {}).get("bytes_per_launch")
             except (OSError, ValueError):
                 ctraffic = None
-        roof = {"bound": "hbm", "kernel": "i8_chain_kernel (whole sweep, one dispatch)", "achieved": round(gbs, 1),
+        ckern = "i8_chain_kernel" if args.m <= 2 else "i8_mt_chain_kernel"
+        roof = {"bound": "hbm", "kernel": f"{ckern} (whole sweep, one dispatch)", "achieved": round(gbs, 1),
                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": ctraffic,
                 "launches": 1, "avg_us": round(ms.value * 1e3, 1), "bytes_per_launch": total_bytes}
     else:

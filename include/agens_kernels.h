@@ -202,8 +202,9 @@ int ak_wq_gemv_kt_silu(int bits, const void* gate_up, int m, const void* wt, con
  *
  * A step has ak_wq_gemv_kt_multi's arguments (ldy[i] = 0: n[i]).  independent = 1 declares that the step reads and
  * writes nothing that the steps since the last dependent step write (or read, for its writes): it then does not wait.
- * The chained kernel takes steps of group 128 with m <= 2 on the default numerics; any other chain runs as one
- * ak_wq_gemv_kt_multi call per step (same results, no overlap).
+ * The chained kernels take steps of group 128 on the default numerics: with m <= 2 the line-load kernel's steps, with
+ * m <= 4 (no act step) the tokens-in-A-rows kernel's; any other chain runs as one ak_wq_gemv_kt_multi call per step
+ * (same results, no overlap).
  *   ak_wq_chain_create  validates the steps (as ak_wq_gemv_kt_multi: 1 on a bad argument), allocates and uploads the
  *                       chain's step table (device memory, synchronous); not under stream capture;
  *   ak_wq_chain_run     one launch on `stream`, allocates nothing, capturable; at most one chained launch may run on

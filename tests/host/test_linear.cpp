@@ -217,7 +217,7 @@ int main() {
         x = o[5].ptr();
       }
       EXPECT(ch.build() == 0, "chain build");
-      EXPECT(ch.chained() == (m <= 2), "chained for 1 and 2 tokens");
+      EXPECT(ch.chained() == (m <= 2), "chained for 1 and 2 tokens (a fused activation step: chained up to 2)");
       EXPECT(ch.add(layers[0].o, h.ptr(), out[0][0][3].ptr(), m) == 1, "add after build -> 1");
       EXPECT(ch.run(nullptr) == 0, "chain run");
       check(ak_synchronize(), "sync");

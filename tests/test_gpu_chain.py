@@ -1,5 +1,6 @@
 """Chained GEMV steps (ak_wq_chain_*) on the GPU: one persistent launch that runs a list of ak_wq_gemv_kt_multi steps
-with grid barriers between them (the MI355X counterpart of the reference's programmatic-dependent-launch chains of
+(1..2 tokens: the line-load kernel's steps; 3..4 tokens: the tokens-in-A-rows kernel's) with grid barriers or tagged
+activations between them (the MI355X counterpart of the reference's programmatic-dependent-launch chains of
 GEMV kernels, kernels/src/runtime.cu:198-230, kernels/include/agens_pdl.cuh:1-16).
 
 Every step here reads what the step before it wrote (decoder-layer data flow: qkv -> o -> gate_up -> down -> next
@@ -111,7 +112,7 @@ def assert_same(got, want, what):
                 raise AssertionError(f"{what}: step {si} segment {j}: {bad} of {a.size} outputs differ")
 
 
-@pytest.mark.parametrize("m", [1, 2])
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
 def test_chain_data_flow_matches_oracle_and_launches(m):
     K = kernels()
     H, KV, INTER = 2048, 256, 2560  # INTER = 2.5 tiles: the padded last tile in down's k
@@ -133,24 +134,25 @@ def test_chain_data_flow_matches_oracle_and_launches(m):
     assert_same(read_outputs(m, flow), want, "launches vs oracle")
 
 
-def test_chain_replays_with_new_inputs():
+@pytest.mark.parametrize("m", [1, 4])
+def test_chain_replays_with_new_inputs(m):
     """Each replay reads the inputs of its own run: a stale read of an earlier run's values would show."""
     K = kernels()
     H, KV, INTER = 1024, 128, 1536
-    h, steps, flow = build(1, [4, 3], H, KV, INTER)
+    h, steps, flow = build(m, [4, 3], H, KV, INTER)
     ch = Chain(steps)
     assert ch.chained
     for rep in range(4):
-        h_host = gen_x(500 + rep, H)
+        h_host = gen_x(500 + rep, m * H)
         check(K.ak_memcpy_h2d(h.p, h_host.ctypes.data, h_host.nbytes), "h2d")
         ch.run()
         if rep == 2:  # a plain launch between chained runs (the flag words persist across launches)
             lins, xin, k, ys = flow[0]
-            gemv(lins[0].bits, xin.p, 1, [l.L for l in lins], k, 128, ys=ys)
+            gemv(lins[0].bits, xin.p, m, [l.L for l in lins], k, 128, ys=ys)
             ch.run()
         check(K.ak_synchronize(), "sync")
         assert K.ak_wq_chain_status() == 0
-        assert_same(read_outputs(1, flow), oracle_flow(h_host, 1, flow), f"replay {rep}")
+        assert_same(read_outputs(m, flow), oracle_flow(h_host, m, flow), f"replay {rep}")
 
 
 def test_chain_independent_steps():
@@ -179,10 +181,10 @@ def test_chain_independent_steps():
 
 
 def test_chain_fallback_runs_steps_one_launch_each():
-    """A group-64 step (and m > 2) cannot run chained: the chain runs one launch per step, same results."""
+    """A group-64 step (and m > 4) cannot run chained: the chain runs one launch per step, same results."""
     K = kernels()
     H, KV, INTER = 1024, 128, 1024
-    for group, m in [(64, 1), (128, 4)]:
+    for group, m in [(64, 1), (64, 4), (128, 5), (128, 9)]:
         h, steps, flow = build(m, [4, 2], H, KV, INTER, group)
         ch = Chain(steps)
         assert not ch.chained
@@ -193,7 +195,7 @@ def test_chain_fallback_runs_steps_one_launch_each():
         assert_same(read_outputs(m, flow), oracle_flow(h_host, m, flow), f"fallback group {group} m {m}")
 
 
-@pytest.mark.parametrize("m", [1, 2])
+@pytest.mark.parametrize("m", [1, 2, 4])
 def test_chain_at_decode_shapes_matches_launches(m):
     """Two 32B-shaped layers (QKV 5120 -> 5120 + 2 x 1024, O, gate_up 5120 -> 55296, down 27648 -> 5120; the down
     steps split k across workgroups): every chained step equals the oracle on its first, middle and last 64 rows of
@@ -306,16 +308,18 @@ def test_chain_at_tp8_rank_shapes_matches_oracle(m):
 def _run_mixed_chain(m, reps, tags):
     """A: x -> y1; B: y1 -> y2 and C: y2 -> y3 (each reads the step just before it: tagged activations); D: y1 -> y4
     (reads A's output, three steps back: a grid-barrier wait, so C signals the flags); E: SiLU(gate) * up of y4 -> y5
-    (reads D's output, fused activation: tagged, k split across workgroups).  Returns every run's outputs."""
+    (reads D's output, fused activation: tagged, k split across workgroups; above two tokens E reads y4 as it is, the
+    chained kernel of 3..8 tokens taking no fused activation).  Returns every run's outputs."""
+    act = 1 if m <= 2 else 0
     K = kernels()
     k, inter = 2048, 16384
     a, b, c = Lin(41, 4096, k, 3), Lin(43, 2048, 4096, 2), Lin(45, 3072, 2048, 4)
-    d, e = Lin(47, 2 * inter, 4096, 3), Lin(49, 1024, inter, 2)
+    d, e = Lin(47, 2 * inter, 4096, 3), Lin(49, 1024, inter if act else 2 * inter, 2)
     x = Dev(m * k * 2)
     ys = [Dev(m * n * 2) for n in (4096, 2048, 3072, 2 * inter, 1024)]
     steps = [wq_step(3, x, m, [a.L], [ys[0]], k), wq_step(2, ys[0], m, [b.L], [ys[1]], 4096),
              wq_step(4, ys[1], m, [c.L], [ys[2]], 2048), wq_step(3, ys[0], m, [d.L], [ys[3]], 4096),
-             wq_step(2, ys[3], m, [e.L], [ys[4]], inter, act=1)]
+             wq_step(2, ys[3], m, [e.L], [ys[4]], inter if act else 2 * inter, act=act)]
     old = os.environ.get("AK_CHAIN_TAGS")
     os.environ["AK_CHAIN_TAGS"] = "1" if tags else "0"
     try:
@@ -341,7 +345,10 @@ def _run_mixed_chain(m, reps, tags):
         for lin, xin, kk, y in ((a, x, k, ys[0]), (b, ys[0], 4096, ys[1]), (c, ys[1], 2048, ys[2]),
                                 (d, ys[0], 4096, ys[3])):
             gemv(lin.bits, xin.p, m, [lin.L], kk, 128, ys=[y])
-        check(K.ak_wq_gemv_kt_silu(2, ys[3].p, m, e.L.wt.p, e.L.st.p, ys[4].p, 1024, 0, inter, 128, None), "silu")
+        if act:
+            check(K.ak_wq_gemv_kt_silu(2, ys[3].p, m, e.L.wt.p, e.L.st.p, ys[4].p, 1024, 0, inter, 128, None), "silu")
+        else:
+            gemv(e.bits, ys[3].p, m, [e.L], 2 * inter, 128, ys=[ys[4]])
         check(K.ak_synchronize(), "sync")
         for si, (g, y, n) in enumerate(zip(got, ys, (4096, 2048, 3072, 2 * inter, 1024))):
             assert np.array_equal(g, y.get(np.uint16, m * n)), f"m={m} run {rep} step {'ABCDE'[si]}"
@@ -349,7 +356,7 @@ def _run_mixed_chain(m, reps, tags):
     return runs
 
 
-@pytest.mark.parametrize("m", [1, 2])
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
 def test_chain_tagged_and_barrier_waits_mix(m):
     """Tagged activation waits beside grid-barrier waits in one chain, on three runs in a row with new inputs (the
     launch tag advances; a stale tag of the run before would read old activations): every step equals one launch per
@@ -399,38 +406,40 @@ def test_chain_tagged_read_of_a_later_segment():
                 assert np.array_equal(g, y.get(np.uint16, m * n)), f"tags {tags} run {rep} step {name}"
 
 
-def test_chain_tag_wraps_after_65536_runs():
+@pytest.mark.parametrize("m", [1, 4])
+def test_chain_tag_wraps_after_65536_runs(m):
     """The 16-bit launch tag of tagged activations wraps after 65536 launches of a chain: the runs around the wrap
     (tag 65535, 0, 1) read their own activations, not the previous run's (each run gets new inputs; equal to one
     launch per step)."""
     K = kernels()
     k = 1024
     a, b = Lin(91, 1024, k, 3), Lin(93, 512, 1024, 4)
-    x = Dev(k * 2)
-    y1, y2 = Dev(1024 * 2), Dev(512 * 2)
-    ch = Chain([wq_step(3, x, 1, [a.L], [y1], k), wq_step(4, y1, 1, [b.L], [y2], 1024)])
+    x = Dev(m * k * 2)
+    y1, y2 = Dev(m * 1024 * 2), Dev(m * 512 * 2)
+    ch = Chain([wq_step(3, x, m, [a.L], [y1], k), wq_step(4, y1, m, [b.L], [y2], 1024)])
     assert ch.chained
-    xh = gen_x(950, k)
+    xh = gen_x(950, m * k)
     check(K.ak_memcpy_h2d(x.p, xh.ctypes.data, xh.nbytes), "h2d")
     for _ in range(65534):  # runs 0 .. 65533 (tags 1 .. 65534)
         ch.run()
     check(K.ak_synchronize(), "sync")
     assert K.ak_wq_chain_status() == 0
     for rep in range(4):  # runs 65534 .. 65537: tags 65535, 0, 1, 2
-        xh = gen_x(951 + rep, k)
+        xh = gen_x(951 + rep, m * k)
         check(K.ak_memcpy_h2d(x.p, xh.ctypes.data, xh.nbytes), "h2d")
         ch.run()
         check(K.ak_synchronize(), "sync")
         assert K.ak_wq_chain_status() == 0
-        got = [y1.get(np.uint16, 1024), y2.get(np.uint16, 512)]
-        gemv(3, x.p, 1, [a.L], k, 128, ys=[y1])
-        gemv(4, y1.p, 1, [b.L], 1024, 128, ys=[y2])
+        got = [y1.get(np.uint16, m * 1024), y2.get(np.uint16, m * 512)]
+        gemv(3, x.p, m, [a.L], k, 128, ys=[y1])
+        gemv(4, y1.p, m, [b.L], 1024, 128, ys=[y2])
         check(K.ak_synchronize(), "sync")
-        assert np.array_equal(got[0], y1.get(np.uint16, 1024)), f"run {65534 + rep}: step 0"
-        assert np.array_equal(got[1], y2.get(np.uint16, 512)), f"run {65534 + rep}: step 1"
+        assert np.array_equal(got[0], y1.get(np.uint16, m * 1024)), f"run {65534 + rep}: step 0"
+        assert np.array_equal(got[1], y2.get(np.uint16, m * 512)), f"run {65534 + rep}: step 1"
 
 
-def test_chain_in_a_graph_replays_with_new_inputs():
+@pytest.mark.parametrize("m", [1, 4])
+def test_chain_in_a_graph_replays_with_new_inputs(m):
     """The chained launch captured in a hipGraph (ak_wq_chain_run is capturable and allocates nothing): three replays,
     each after new inputs were copied in with an eager synchronous copy, each equal to one launch per step (the launch
     tag advances inside the kernel, so every replay reads its own tagged activations)."""
@@ -439,10 +448,10 @@ def test_chain_in_a_graph_replays_with_new_inputs():
     vp = ctypes.c_void_p
     k = 2048
     a, b, c = Lin(101, 2048, k, 3), Lin(103, 1024, 2048, 2), Lin(105, 768, 1024, 4)
-    x = Dev(k * 2)
-    y1, y2, y3 = Dev(2048 * 2), Dev(1024 * 2), Dev(768 * 2)
-    ch = Chain([wq_step(3, x, 1, [a.L], [y1], k), wq_step(2, y1, 1, [b.L], [y2], 2048),
-                wq_step(4, y2, 1, [c.L], [y3], 1024)])
+    x = Dev(m * k * 2)
+    y1, y2, y3 = Dev(m * 2048 * 2), Dev(m * 1024 * 2), Dev(m * 768 * 2)
+    ch = Chain([wq_step(3, x, m, [a.L], [y1], k), wq_step(2, y1, m, [b.L], [y2], 2048),
+                wq_step(4, y2, m, [c.L], [y3], 1024)])
     assert ch.chained
     stream, graph, exe = vp(), vp(), vp()
     assert hip.hipStreamCreate(ctypes.byref(stream)) == 0
@@ -453,18 +462,18 @@ def test_chain_in_a_graph_replays_with_new_inputs():
         check(rc, "ak_wq_chain_run under capture")
         assert hip.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, ctypes.c_size_t(0)) == 0
         for rep in range(3):
-            xh = gen_x(1100 + rep, k)
+            xh = gen_x(1100 + rep, m * k)
             check(K.ak_memcpy_h2d(x.p, xh.ctypes.data, xh.nbytes), "h2d")
             assert hip.hipGraphLaunch(exe, stream) == 0
             assert hip.hipStreamSynchronize(stream) == 0
             assert K.ak_wq_chain_status() == 0
-            got = [y.get(np.uint16, n) for y, n in ((y1, 2048), (y2, 1024), (y3, 768))]
-            gemv(3, x.p, 1, [a.L], k, 128, ys=[y1])
-            gemv(2, y1.p, 1, [b.L], 2048, 128, ys=[y2])
-            gemv(4, y2.p, 1, [c.L], 1024, 128, ys=[y3])
+            got = [y.get(np.uint16, m * n) for y, n in ((y1, 2048), (y2, 1024), (y3, 768))]
+            gemv(3, x.p, m, [a.L], k, 128, ys=[y1])
+            gemv(2, y1.p, m, [b.L], 2048, 128, ys=[y2])
+            gemv(4, y2.p, m, [c.L], 1024, 128, ys=[y3])
             check(K.ak_synchronize(), "sync")
             for g, (y, n, name) in zip(got, ((y1, 2048, "A"), (y2, 1024, "B"), (y3, 768, "C"))):
-                assert np.array_equal(g, y.get(np.uint16, n)), f"replay {rep} step {name}"
+                assert np.array_equal(g, y.get(np.uint16, m * n)), f"replay {rep} step {name}"
     finally:
         if exe:
             hip.hipGraphExecDestroy(exe)
