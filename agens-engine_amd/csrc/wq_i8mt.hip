@@ -468,7 +468,7 @@ __device__ __forceinline__ void mt_body(const I8Args& a, uint8_t* lds, bool wait
     } else if constexpr (SK) {  // to the range's partials, device-coherent (the range's last workgroup adds them)
 #pragma unroll
       for (int tg = 0; tg < NT; ++tg)
-        __hip_atomic_store(spart + ((size_t)(ep * MP + 4 * tg + h) * n_b16 + b_lo + eg) * 16 + c, pp[tg],
+        __hip_atomic_store(spart + (((size_t)ep * n_b16 + b_lo + eg) * MP + 4 * tg + h) * 16 + c, pp[tg],
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     } else if constexpr (SPLIT == 1) {
 #pragma unroll
@@ -544,7 +544,7 @@ __device__ __forceinline__ void mt_body(const I8Args& a, uint8_t* lds, bool wait
     __syncthreads();  // every thread has read the flag before the outputs overwrite it
     for (int i = tid; i < nb * MP * 16; i += 64 * nwv) {
       const int bl = i / (MP * 16), o = i - bl * MP * 16, t = o >> 4;
-      const size_t off = ((size_t)t * n_b16 + b_lo + bl) * 16 + (o & 15);
+      const size_t off = ((size_t)(b_lo + bl) * MP + t) * 16 + (o & 15);
       yl[i] = f2bf(sum_stripe_partials(spart, off, (size_t)MP * n_b16 * 16, P));
     }
   }

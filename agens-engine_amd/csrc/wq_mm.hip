@@ -68,7 +68,7 @@ struct MmArgs {
   int tl;         // tokens per (group, k-step, chunk) row of the image: 4, 8 or 16 (one tile), 16 per tile above
   int cq;         // quads per chunk of the activation image
   int wg_end[4];  // workgroups of segments 0..i
-  float* part;    // SK: stripe partials [P][16 NTT][rows] per segment, and one counter per row range
+  float* part;    // SK: stripe partials [P][16-row blocks][16 NTT tokens][16 rows] per segment, and one counter per row range
   int* cnt;
   int act;        // 1: x is the merged gate_up [m][2k] and the activations are SiLU(gate) * up (wq_silu.h)
 };
@@ -450,7 +450,7 @@ __global__ void __launch_bounds__(mm_waves<NTT>() * 64, 1) mm_kernel(const MmArg
     // counter moves; the range's last workgroup adds the P partials of each output in stripe order
     for (int i = tid; i < nb * MP * 16; i += blockDim.x) {
       const int bl = i / (MP * 16), o = i - bl * MP * 16, t = o >> 4;
-      __hip_atomic_store(spart + ((size_t)(psk * MP + t) * n_b16 + b_lo + bl) * 16 + (o & 15),
+      __hip_atomic_store(spart + (((size_t)psk * n_b16 + b_lo + bl) * MP + t) * 16 + (o & 15),
                          reinterpret_cast<const float*>(outl)[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __builtin_amdgcn_s_waitcnt(kVmcnt0);
@@ -466,7 +466,7 @@ __global__ void __launch_bounds__(mm_waves<NTT>() * 64, 1) mm_kernel(const MmArg
     for (int i = tid; i < nb * MP * 16; i += blockDim.x) {
       const int bl = i / (MP * 16), o = i - bl * MP * 16, t = o >> 4, row = (b_lo + bl) * 16 + (o & 15);
       if (t >= m || row >= n) continue;
-      const size_t off = ((size_t)t * n_b16 + b_lo + bl) * 16 + (o & 15);
+      const size_t off = ((size_t)(b_lo + bl) * MP + t) * 16 + (o & 15);
       yseg[(size_t)t * ldy + row] = f2bf(sum_stripe_partials(spart, off, (size_t)MP * n_b16 * 16, P));
     }
   }
