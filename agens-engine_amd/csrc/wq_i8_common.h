@@ -44,6 +44,28 @@ __device__ __forceinline__ float sum_stripe_partials(const float* base, size_t o
   return y;
 }
 
+// The same for U outputs at once: the loads of all of them are requested before any sum.
+template <int U>
+__device__ __forceinline__ void sum_stripe_partials_n(const float* base, const size_t (&off)[U], size_t stride, int P,
+                                                      float (&y)[U]) {
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, 0x7FFFFFFF, 0x00020000);
+  float v[U][8];
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      v[u][q] = q < P ? __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (int)((off[u] + q * stride) * 4), 0, 16))
+                      : 0.f;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    y[u] = v[u][0];
+#pragma unroll
+    for (int q = 1; q < 8; ++q)
+      if (q < P) y[u] += v[u][q];
+  }
+}
+
 // Stripes are contiguous runs of whole 1024-input tiles: with nt = nquad / qpt tiles, P = min(8, nt) stripes and stripe
 // p = tiles [p * nt / P, (p + 1) * nt / P), i.e. quads [qpt * (p * nt / P), qpt * ((p + 1) * nt / P)).
 __host__ __device__ inline int stripe_count(int nquad, int qpt) { return nquad / qpt < 8 ? nquad / qpt : 8; }

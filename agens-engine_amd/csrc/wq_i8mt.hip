@@ -159,6 +159,9 @@ __device__ __forceinline__ void mt_body(const I8Args& a, uint8_t* lds, bool wait
       if (i < sg) spart += (size_t)P * MP * ((AK_PICK(i, sgs.n) + 15) >> 4) * 16;
     scnt += wg0 / P + r;
   }
+  // the segment's stripe partials as a buffer (below 2 GB: P x tokens x rows x 4 B)
+  const __amdgpu_buffer_rsrc_t rpart = __builtin_amdgcn_make_buffer_rsrc(spart, (short)0, 0x7FFFFFFF, kRsrcWord3);
+  (void)rpart;
 
   // chunks of stripes and the groups an activation image holds (the largest chunk's)
   const int nch = CH ? a.nb : 1;
@@ -466,10 +469,12 @@ __device__ __forceinline__ void mt_body(const I8Args& a, uint8_t* lds, bool wait
 #pragma unroll
       for (int tg = 0; tg < NT; ++tg) part[((eg * P + ep) * MP + 4 * tg + h) * 16 + c] = pp[tg];
     } else if constexpr (SK) {  // to the range's partials, device-coherent (the range's last workgroup adds them)
+      // (block-major: [stripe][block][token][row]; a buffer store with the block's offset scalar and the lane's part a
+      // per-lane constant, device-coherent as an agent-scope atomic store)
+      const int so = ((ep * n_b16 + b_lo + eg) * MP * 16) * 4;
 #pragma unroll
       for (int tg = 0; tg < NT; ++tg)
-        __hip_atomic_store(spart + (((size_t)ep * n_b16 + b_lo + eg) * MP + 4 * tg + h) * 16 + c, pp[tg],
-                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(pp[tg]), rpart, ((4 * tg + h) * 16 + c) * 4, so, kSc1);
     } else if constexpr (SPLIT == 1) {
 #pragma unroll
       for (int tg = 0; tg < NT; ++tg) {
@@ -542,10 +547,22 @@ __device__ __forceinline__ void mt_body(const I8Args& a, uint8_t* lds, bool wait
     __syncthreads();
     if (!*last) return;
     __syncthreads();  // every thread has read the flag before the outputs overwrite it
-    for (int i = tid; i < nb * MP * 16; i += 64 * nwv) {
-      const int bl = i / (MP * 16), o = i - bl * MP * 16, t = o >> 4;
-      const size_t off = ((size_t)(b_lo + bl) * MP + t) * 16 + (o & 15);
-      yl[i] = f2bf(sum_stripe_partials(spart, off, (size_t)MP * n_b16 * 16, P));
+    // two outputs per thread at a time (their partials' loads in flight together; block-major partials: the
+    // workgroup's outputs are the contiguous run from b_lo * MP * 16, in yl's order)
+    // (two token groups: one at a time, as two spill the W2 kernel's registers)
+    const int ne = nb * MP * 16, st = 64 * nwv;
+    if constexpr (NT == 2) {
+      for (int i = tid; i < ne; i += st)
+        yl[i] = f2bf(sum_stripe_partials(spart, (size_t)b_lo * MP * 16 + i, (size_t)MP * n_b16 * 16, P));
+    } else {
+      for (int i0 = tid; i0 < ne; i0 += 2 * st) {
+        const size_t o0 = (size_t)b_lo * MP * 16 + i0, o1 = (size_t)b_lo * MP * 16 + (i0 + st < ne ? i0 + st : i0);
+        const size_t off[2] = {o0, o1};
+        float y[2];
+        sum_stripe_partials_n<2>(spart, off, (size_t)MP * n_b16 * 16, P, y);
+        yl[i0] = f2bf(y[0]);
+        if (i0 + st < ne) yl[i0 + st] = f2bf(y[1]);
+      }
     }
   }
   if constexpr (CH) {

@@ -463,11 +463,19 @@ __global__ void __launch_bounds__(mm_waves<NTT>() * 64, 1) mm_kernel(const MmArg
     }
     __syncthreads();
     if (!*last) return;
-    for (int i = tid; i < nb * MP * 16; i += blockDim.x) {
-      const int bl = i / (MP * 16), o = i - bl * MP * 16, t = o >> 4, row = (b_lo + bl) * 16 + (o & 15);
-      if (t >= m || row >= n) continue;
-      const size_t off = ((size_t)(b_lo + bl) * MP + t) * 16 + (o & 15);
-      yseg[(size_t)t * ldy + row] = f2bf(sum_stripe_partials(spart, off, (size_t)MP * n_b16 * 16, P));
+    // two outputs per thread at a time (block-major partials: the workgroup's outputs are the contiguous run from
+    // b_lo * MP * 16); padding tokens and rows past n are summed and not written
+    const int ne = nb * MP * 16, st = blockDim.x;
+    for (int i0 = tid; i0 < ne; i0 += 2 * st) {
+      const size_t off[2] = {(size_t)b_lo * MP * 16 + i0, (size_t)b_lo * MP * 16 + (i0 + st < ne ? i0 + st : i0)};
+      float y[2];
+      sum_stripe_partials_n<2>(spart, off, (size_t)MP * n_b16 * 16, P, y);
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int i = i0 + u * st;
+        const int bl = i / (MP * 16), o = i - bl * MP * 16, t = o >> 4, row = (b_lo + bl) * 16 + (o & 15);
+        if (i < ne && t < m && row < n) yseg[(size_t)t * ldy + row] = f2bf(y[u]);
+      }
     }
   }
 }
