@@ -6,26 +6,34 @@
 // kernels/src/bf16_linear.cu:68-92).  Here the KT records are read once per token tile, expanded to bf16 in registers
 // and written to LDS, and v_mfma_f32_16x16x32_bf16 consumes them there: no scratch, no second pass over the weights.
 //
-// Tiles: a workgroup (256 threads, 4 waves; two per CU) owns 128 output rows x 128 tokens and walks k in 64-input
-// slabs:
-//   - loads, kRing - 1 slabs ahead in a ring of registers: thread (row tid / 2, half tid % 2) loads its lane chunk of
-//     the slab from the row's KT record (W4 16 B, W3 8 + 4 B, W2 8 B) and the group's scale; the inputs are 1024
-//     16-byte chunks per slab, 8 consecutive threads reading one token's 128 bytes.  Raw buffer loads with a per-lane
-//     offset fixed for the kernel and a scalar per-slab offset keep address arithmetic off the vector unit; no load
-//     sits under a branch (the compiler's wait counts stay exact, so the ring stays full);
-//   - LDS (two stages of 16 KB weights + 16 KB inputs): rows / tokens of 64 bf16 (128 B); the 16-byte chunk q of row
-//     r sits at slot q ^ ((r >> 1) & 7), so the 16 rows of one MFMA operand read hit 16 distinct 16-byte bank slots;
-//   - compute: wave w owns rows 64 (w & 1) .. +63 and tokens 64 (w >> 1) .. +63, 4 x 4 MFMA tiles of 16 x 16, two
-//     32-input slices per slab; lane l reads 8 inputs 8 (l / 16) .. of its slice for row / token l % 16 (the same
-//     input-to-slot map for weights and tokens, which is all an MFMA needs).
+// Two tilings, one kernel template (wq_gemm_kernel<BITS, G, R, T, RING, XR, XM, DMA>); k is walked in 64-input slabs.
+//   - 128 x 128 (R = T = 128; 256 threads, 4 waves, two workgroups per CU), where few tiles exist (narrow linears):
+//     thread (row tid / 2, half tid % 2) loads its lane chunk of the slab from the row's KT record (W4 16 B, W3
+//     8 + 4 B, W2 8 B) and the group's scale, RING - 1 slabs ahead in a ring of registers; the inputs are 1024 16-byte
+//     chunks per slab, 8 consecutive threads reading one token's 128 bytes, XR - 1 slabs ahead; both are written to
+//     two LDS stages (16 KB weights, dequantized, + 16 KB inputs).  Grid: row tile major with the token tiles of a row
+//     tile 8 workgroups apart (same XCD: workgroup i runs on XCD i % 8), sharing the row tile's weights in that L2.
+//   - 256 x 256 (R = T = 256; 512 threads, 8 waves, one workgroup per CU), where the tiles fill the GPU (wide linears,
+//     or from 2048 tokens): each weight is dequantized once per 256 tokens.  The tokens go straight from the buffer
+//     into LDS (buffer loads into LDS, two stages of 32 KB, one slab ahead; no registers), the weights through a
+//     register ring 3 slabs ahead into two 32 KB stages; the next slab's dequantization is interleaved with this
+//     slab's MFMAs (after each 16 MFMAs one of its four words; one MFMA, three VALU instructions alternating), since
+//     the two waves of a SIMD leave the slab's barrier together.  Grid: the tiles in token-major order cut into 8
+//     contiguous runs, XCD x taking run x, so that each XCD works on one or two token tiles (256 tokens x k inputs)
+//     that stay in its L2 while the weights stream.
+// Common: raw buffer loads with a per-lane offset fixed for the kernel and a scalar per-slab offset keep address
+// arithmetic off the vector unit; no load sits under a branch (the compiler's wait counts stay exact).  LDS rows /
+// tokens of 64 bf16 (128 B): the 16-byte chunk q of row r sits at slot q ^ ((r >> 1) & 7), so the 16 rows of one MFMA
+// operand read hit 16 distinct 16-byte bank slots.  Wave tiles of 64 rows x 64 (128 x 128) or 128 (256 x 256)
+// tokens, 16 x 16 MFMA tiles, two 32-input slices per slab; lane l reads 8 inputs 8 (l / 16) .. of its slice for row /
+// token l % 16 (the same input-to-slot map for weights and tokens, which is all an MFMA needs).
 // The accumulation order is this kernel's own (fp32 MFMA sums over 32 inputs, slabs in order): results agree with the
 // reference's cuBLAS route and with the oracle's dequantized weights times x in fp64 within fp32-accumulation error.
-// Grid: row tile major with the token tiles of a row tile 8 workgroups apart (same XCD: workgroup i runs on XCD
-// i % 8), so the token tiles of one row tile share its weights through that XCD's L2.
 #include <type_traits>
 
 #include "agens_kernels.h"
 #include "wq_common.h"
+
 
 namespace agq {
 namespace {
@@ -34,10 +42,8 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-// a workgroup: kRows output rows x kToks tokens, 64-input slabs, wave tiles of 64 x 64 (kRows / 64 x 2 waves)
-constexpr int kRows = 128, kToks = 128, kSlab = 64, kThreads = kRows * 2, kStages = 2, kRing = 4;
-constexpr int kRowBytes = kSlab * 2;                 // one row / token of a slab in LDS
-constexpr int kStage = (kRows + kToks) * kRowBytes;
+// slabs of 64 inputs (one row / token of a slab: 128 B in LDS), two LDS stages
+constexpr int kSlab = 64, kRowBytes = kSlab * 2, kStages = 2;
 constexpr int kRsrcWord3 = 0x00020000;  // raw buffer resource, dword 3 (CDNA)
 
 // f(integral_constant<int, I>) for I = B .. E - 1, unrolled at compile time
@@ -57,6 +63,11 @@ struct ChunkRaw {
   u32x4 w;  // W4: the chunk; W3: lo words in 0, 1 and the third-bit word in 2; W2: lo words in 0, 1
   uint32_t s;
 };
+
+// 16 bytes per lane from a buffer straight into LDS: lane l writes dst + 16 l (dst the same for the whole wave)
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, uint8_t* dst, int voff, int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, voff, soff, 0, 0);
+}
 
 // Morton spreading of 2-bit / 1-bit fields into nibbles (as the repack's inverse)
 __device__ __forceinline__ uint32_t spread2(uint32_t v) {
@@ -104,18 +115,38 @@ __device__ __forceinline__ u32x4 dequant8(uint32_t w, float s) {
   return u32x4{o[0], o[1], o[2], o[3]};
 }
 
-template <int BITS, int G>
-__global__ void __launch_bounds__(kThreads, 2) wq_gemm_kernel(const uint16_t* __restrict__ x, int m,
+// R output rows x T tokens per workgroup (2 R threads: a thread pair per row), wave tiles of 64 rows x WT tokens,
+// loads of the weights RING - 1 slabs ahead and of the tokens XR - 1 slabs ahead (RING a multiple of XR); XM: the
+// XCD-contiguous tile order (below); DMA: the tokens are loaded straight into XR LDS stages of their own (buffer
+// loads into LDS), not through registers
+template <int BITS, int G, int R, int T, int RING, int XR, bool XM, bool DMA>
+__global__ void __launch_bounds__(2 * R, R == 128 ? 2 : 1) wq_gemm_kernel(const uint16_t* __restrict__ x, int m,
                                                               const uint8_t* __restrict__ wt,
                                                               const uint16_t* __restrict__ st,
                                                               uint16_t* __restrict__ y, int n, int ldy, int k,
-                                                              int ntok_tiles) {
+                                                              int nrow_tiles, int ntok_tiles) {
+  constexpr int kRows = R, kToks = T, kThreads = 2 * R, kRing = RING;
+  // LDS: DMA: two weight stages of R rows, then XR token stages of T tokens; else two stages of R rows + T tokens
+  constexpr int kStage = DMA ? R * kRowBytes : (R + T) * kRowBytes, kXBase = DMA ? 2 * kStage : R * kRowBytes;
+  constexpr int kXStage = DMA ? T * kRowBytes : kStage;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   constexpr int OFF = BITS == 4 ? 8 : BITS == 3 ? 4 : 2;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  // workgroup -> (row tile, token tile): blocks of 8 row tiles x all token tiles, the token tiles of a row tile 8 apart
-  const int b = blockIdx.x, grp = b / (8 * ntok_tiles), in = b - grp * 8 * ntok_tiles;
-  const int rt = grp * 8 + (in & 7), tt = in >> 3;
+  // workgroup -> (row tile, token tile).  Workgroup b runs on XCD b % 8.  XM: the tiles in token-major order
+  // (tile = token tile x row tiles + row tile) cut into 8 contiguous runs, XCD x taking run x, so that each XCD's
+  // workgroups share one or two token tiles (T tokens x k inputs) through its L2 while the weights stream; else blocks
+  // of 8 row tiles x all token tiles with the token tiles of a row tile 8 workgroups apart (same XCD: they share the
+  // row tile's weights).
+  const int b = blockIdx.x;
+  int rt, tt;
+  if constexpr (XM) {
+    const int per = (nrow_tiles * ntok_tiles + 7) >> 3, tile = (b & 7) * per + (b >> 3);
+    tt = tile / nrow_tiles, rt = tile - tt * nrow_tiles;
+    if (tt >= ntok_tiles) return;
+  } else {
+    const int grp = b / (8 * ntok_tiles), in = b - grp * 8 * ntok_tiles;
+    rt = grp * 8 + (in & 7), tt = in >> 3;
+  }
   const int o0 = rt * kRows, t0 = tt * kToks;
   if (o0 >= n || t0 >= m) return;  // the last group of 8 row tiles may be partial
 
@@ -136,26 +167,40 @@ __global__ void __launch_bounds__(kThreads, 2) wq_gemm_kernel(const uint16_t* __
                                                                       kRsrcWord3);
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(st), (short)0, 0x7FFFFFFF,
                                                                       kRsrcWord3);
-  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(x), (short)0, 0x7FFFFFFF,
-                                                                      kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(x), (short)0,
+                                                                      DMA ? m * k * 2 : 0x7FFFFFFF, kRsrcWord3);
   const int vw = orow * REC + lj * CB, vh = orow * REC + 256 + lj * 4, vs = orow * (1024 / G) * 2;
-  int vx[XPT];
+  // register path: chunk c = tid + j kThreads is (token c / 8, chunk c % 8), tokens past m read token 0.  DMA:
+  // instruction j of wave w fills the 1 KB block b = w + (kThreads / 64) j of the stage (tokens 8 b .. 8 b + 7, 128 B
+  // each), lane l writing bytes 16 l .. 16 l + 15, i.e. token 8 b + l / 8 at slot l % 8, which holds the token's chunk
+  // (l % 8) ^ ((token >> 1) & 7); one offset vx[0] for all j (+ j x the block step), tokens past m reading zeros
+  // through the buffer's range (m k 2 bytes)
+  int vx[DMA ? 1 : XPT];
+  if constexpr (DMA) {
+    const int tk = 8 * wave + (lane >> 3), q = (lane & 7) ^ ((tk >> 1) & 7);  // ((tk + 64 j) >> 1) & 7 is the same
+    vx[0] = ((t0 + tk) * k + 8 * q) * 2;
+  } else {
 #pragma unroll
-  for (int j = 0; j < XPT; ++j) {
-    const int c = tid + j * kThreads, tk = c >> 3;
-    vx[j] = ((t0 + tk < m ? t0 + tk : 0) * k + 8 * (c & 7)) * 2;
+    for (int j = 0; j < XPT; ++j) {
+      const int c = tid + j * kThreads, tk = c >> 3;
+      vx[j] = ((t0 + tk < m ? t0 + tk : 0) * k + 8 * (c & 7)) * 2;
+    }
   }
   const bool full = t0 + kToks <= m;  // every token of the tile exists (no zero selection)
   int xsel[XPT];                      // else: per chunk, whether its token exists
 #pragma unroll
   for (int j = 0; j < XPT; ++j) xsel[j] = t0 + ((tid + j * kThreads) >> 3) < m;
 
-  struct Slab {
+  struct WSlab {
     ChunkRaw<BITS> w;
+  };
+  struct XSlab {
     u32x4 xv[XPT];
   };
-  Slab rg[kRing];
-  auto issue = [&](int sl, Slab& d) __attribute__((always_inline)) {
+  static_assert(RING % XR == 0, "the token ring must divide the weight ring");
+  WSlab rg[kRing];
+  XSlab rx_[DMA ? 1 : XR];
+  auto issue_w = [&](int sl, WSlab& d) __attribute__((always_inline)) {
     const int t = sl >> 4, s16 = sl & 15;  // tile, slab within the tile
     const int tb = t * n * REC;
     if constexpr (BITS == 4) {
@@ -167,11 +212,21 @@ __global__ void __launch_bounds__(kThreads, 2) wq_gemm_kernel(const uint16_t* __
       d.w.w = u32x4{lo[0], lo[1], hi, 0u};
     }
     d.w.s = __builtin_amdgcn_raw_buffer_load_b16(rs, vs, (t * n * (1024 / G) + (G == 128 ? s16 >> 1 : s16)) * 2, 0);
+  };
+  auto issue_x = [&](int sl, XSlab& d) __attribute__((always_inline)) {
 #pragma unroll
-    for (int j = 0; j < XPT; ++j) d.xv[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, vx[j], sl * kSlab * 2, 0);
+    for (int j = 0; j < XPT; ++j)
+      if constexpr (!DMA) d.xv[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, vx[j], sl * kSlab * 2, 0);
+  };
+  // DMA: slab sl's tokens into token stage xs (every wave its XPT blocks)
+  auto dma_x = [&](int sl, int xs) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < XPT; ++j)
+      lds_dma16(rx, lds + kXBase + xs * kXStage + (wave + (kThreads / 64) * j) * 1024,
+                vx[0] + j * (kThreads / 64) * 8 * k * 2, sl * kSlab * 2);
   };
   // (the zero selection of tokens past m happens here, at the write: selecting at the load would wait for the data)
-  auto put = [&](const Slab& d, int stage) __attribute__((always_inline)) {
+  auto put = [&](const WSlab& d, const XSlab& dx, int stage) __attribute__((always_inline)) {
     uint8_t* base = lds + stage * kStage;
     uint32_t nw[4];
     chunk_codes<BITS>(d.w, nw);
@@ -180,76 +235,153 @@ __global__ void __launch_bounds__(kThreads, 2) wq_gemm_kernel(const uint16_t* __
     for (int u = 0; u < 4; ++u) {
       *reinterpret_cast<u32x4*>(base + swz(lr, 4 * lj + u)) = dequant8<OFF>(nw[u], s);
     }
-    uint8_t* xb = base + kRows * kRowBytes;
+    if constexpr (DMA) return;
+    uint8_t* xb = lds + kXBase + stage * kXStage;
     if (full) {
 #pragma unroll
       for (int j = 0; j < XPT; ++j) {
         const int c = tid + j * kThreads;
-        *reinterpret_cast<u32x4*>(xb + swz(c >> 3, c & 7)) = d.xv[j];
+        *reinterpret_cast<u32x4*>(xb + swz(c >> 3, c & 7)) = dx.xv[j];
       }
     } else {
       const u32x4 z = {0u, 0u, 0u, 0u};
 #pragma unroll
       for (int j = 0; j < XPT; ++j) {
         const int c = tid + j * kThreads;
-        *reinterpret_cast<u32x4*>(xb + swz(c >> 3, c & 7)) = xsel[j] ? d.xv[j] : z;
+        *reinterpret_cast<u32x4*>(xb + swz(c >> 3, c & 7)) = xsel[j] ? dx.xv[j] : z;
       }
     }
   };
 
-  // wave tiles of 64 rows x 64 tokens
-  constexpr int RW = kRows / 64;  // waves along the rows
-  const int wr = (wave % RW) * 64, wtk = (wave / RW) * 64;
+  // wave tiles of 64 rows x WT tokens
+  constexpr int RW = kRows / 64, WT = kToks / (kThreads / 64 / RW), NJ = WT / 16;  // waves along the rows
+  const int wr = (wave % RW) * 64, wtk = (wave / RW) * WT;
   const int lrow = lane & 15, lsub = lane >> 4;
-  f32x4 acc[4][4];
+  f32x4 acc[4][NJ];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < NJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  auto compute = [&](int stage) __attribute__((always_inline)) {
+  auto compute = [&](int stage, int xs) __attribute__((always_inline)) {
     const uint8_t* A = lds + stage * kStage;
-    const uint8_t* B = A + kRows * kRowBytes;
+    const uint8_t* B = lds + kXBase + xs * kXStage;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {  // 32-input slices of the slab
       const int q = 4 * h + lsub;
-      bf16x8 av[4], bv[4];
+      bf16x8 av[4], bv[NJ];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        av[i] = *reinterpret_cast<const bf16x8*>(A + swz(wr + 16 * i + lrow, q));
-        bv[i] = *reinterpret_cast<const bf16x8*>(B + swz(wtk + 16 * i + lrow, q));
-      }
+      for (int i = 0; i < 4; ++i) av[i] = *reinterpret_cast<const bf16x8*>(A + swz(wr + 16 * i + lrow, q));
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) bv[j] = *reinterpret_cast<const bf16x8*>(B + swz(wtk + 16 * j + lrow, q));
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[i], bv[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < NJ; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[i], bv[j], acc[i][j], 0, 0, 0);
     }
   };
 
-  // Pipeline over slabs: two LDS stages and kRing register sets.  Iteration sl: barrier (slab sl in LDS; every wave
-  // done with slab sl - 1), issue the loads of slab sl + kRing - 1, compute slab sl from its stage, write slab sl + 1
-  // (dequantized) into the other stage.
-  constexpr int D = kRing - 1;
+  // compute(stage, xs) with put's weight half interleaved (DMA path): after each 16 MFMAs one of the next slab's four
+  // words is dequantized and written, the MFMAs and that VALU work alternating in each region (a wave issues in
+  // order, so VALU work placed between its MFMAs runs while they do)
+  auto compute_put = [&](int stage, int xs, const WSlab& d, int wstage) __attribute__((always_inline)) {
+    const uint8_t* A = lds + stage * kStage;
+    const uint8_t* B = lds + kXBase + xs * kXStage;
+    uint8_t* base = lds + wstage * kStage;
+    uint32_t nw[4];
+    chunk_codes<BITS>(d.w, nw);
+    const float sc = bf2f(d.w.s);
 #pragma unroll
-  for (int i = 0; i < D; ++i) issue(i < nslab ? i : nslab - 1, rg[i]);
-  put(rg[0], 0);
-  auto iter = [&](int sl, auto S) __attribute__((always_inline)) {
-    constexpr int r1 = (decltype(S)::value + 1) % kRing, rd = (decltype(S)::value + D) % kRing;
-    __syncthreads();
-    issue(sl + D < nslab ? sl + D : nslab - 1, rg[rd]);
-    compute(sl & 1);
-    if (sl + 1 < nslab) put(rg[r1], (sl + 1) & 1);
+    for (int h = 0; h < 2; ++h) {
+      const int q = 4 * h + lsub;
+      bf16x8 av[4], bv[NJ];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) av[i] = *reinterpret_cast<const bf16x8*>(A + swz(wr + 16 * i + lrow, q));
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) bv[j] = *reinterpret_cast<const bf16x8*>(B + swz(wtk + 16 * j + lrow, q));
+#pragma unroll
+      for (int ih = 0; ih < 2; ++ih) {
+#pragma unroll
+        for (int i = 2 * ih; i < 2 * ih + 2; ++i)
+#pragma unroll
+          for (int j = 0; j < NJ; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[i], bv[j], acc[i][j], 0, 0, 0);
+        const int u = 2 * h + ih;
+        *reinterpret_cast<u32x4*>(base + swz(lr, 4 * lj + u)) = dequant8<OFF>(nw[u], sc);
+        static_for<0, 2 * NJ>([&](auto) __attribute__((always_inline)) {
+          __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x0002, 3, 0);  // 1 MFMA, 3 VALU
+        });
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
   };
-  int sl = 0;
-  for (; sl + kRing <= nslab; sl += kRing)
-    static_for<0, kRing>([&](auto I) __attribute__((always_inline)) { iter(sl + decltype(I)::value, I); });
-  static_for<0, kRing - 1>([&](auto I) __attribute__((always_inline)) {
-    if (sl + decltype(I)::value < nslab) iter(sl + decltype(I)::value, I);
-  });
+
+  // Pipeline over slabs: two LDS stages, kRing weight register sets and XR token register sets.  Iteration sl:
+  // barrier (slab sl in LDS; every wave done with slab sl - 1), issue the token loads of slab sl + XR - 1 and then the
+  // weight loads of slab sl + kRing - 1 (in this order: the loads' counter is in order, and the tokens, read from L2,
+  // are needed first), compute slab sl from its stage, write slab sl + 1 (dequantized) into the other stage.
+  constexpr int D = kRing - 1, DX = XR - 1;
+  if constexpr (DMA) {
+    // Iteration sl: wait for this wave's token DMA of slab sl (the loads' counter is in order: at most NAFTER loads
+    // were issued after it), barrier (every wave's DMA of slab sl landed; every wave done with slab sl - 1), DMA of
+    // slab sl + DX into the token stage slab sl - 1 used, weight loads of slab sl + D, compute slab sl, write slab
+    // sl + 1's weights (dequantized) into the other weight stage.
+    constexpr int NW = BITS == 3 ? 3 : 2, NAFTER = NW + (DX - 1) * (XPT + NW);
+    static_assert(DX >= 1 && NAFTER < 64, "token DMA pipeline");
+    constexpr int kWait = (NAFTER & 15) | ((NAFTER >> 4) << 14) | (7 << 4) | (15 << 8);
+#pragma unroll
+    for (int i = 0; i < DX; ++i) dma_x(i < nslab ? i : nslab - 1, i);
+#pragma unroll
+    for (int i = 0; i < D; ++i) issue_w(i < nslab ? i : nslab - 1, rg[i]);
+    put(rg[0], rx_[0], 0);
+    auto iter = [&](int sl, auto S, bool last_ok) __attribute__((always_inline)) {
+      constexpr int r1 = (decltype(S)::value + 1) % kRing, rd = (decltype(S)::value + D) % kRing;
+      constexpr int xc = decltype(S)::value % XR, xd = (decltype(S)::value + DX) % XR;
+      __builtin_amdgcn_s_waitcnt(kWait);
+      __syncthreads();
+      dma_x(sl + DX < nslab ? sl + DX : nslab - 1, xd);
+      issue_w(sl + D < nslab ? sl + D : nslab - 1, rg[rd]);
+      if (last_ok) {
+        compute_put(sl & 1, xc, rg[r1], (sl + 1) & 1);
+      } else {
+        compute(sl & 1, xc);
+        if (sl + 1 < nslab) put(rg[r1], rx_[0], (sl + 1) & 1);
+      }
+    };
+    int sl = 0;
+    for (; sl + kRing < nslab; sl += kRing)  // every iteration here has a next slab
+      static_for<0, kRing>([&](auto I) __attribute__((always_inline)) { iter(sl + decltype(I)::value, I, true); });
+    static_for<0, kRing>([&](auto I) __attribute__((always_inline)) {
+      if (sl + decltype(I)::value < nslab) iter(sl + decltype(I)::value, I, false);
+    });
+  } else {
+#pragma unroll
+    for (int i = 0; i < DX; ++i) issue_x(i < nslab ? i : nslab - 1, rx_[i]);
+#pragma unroll
+    for (int i = 0; i < D; ++i) issue_w(i < nslab ? i : nslab - 1, rg[i]);
+    put(rg[0], rx_[0], 0);
+    auto iter = [&](int sl, auto S) __attribute__((always_inline)) {
+      constexpr int r1 = (decltype(S)::value + 1) % kRing, rd = (decltype(S)::value + D) % kRing;
+      constexpr int x1 = (decltype(S)::value + 1) % XR, xd = (decltype(S)::value + DX) % XR;
+      __syncthreads();
+      if constexpr (DX > 0) issue_x(sl + DX < nslab ? sl + DX : nslab - 1, rx_[xd]);
+      issue_w(sl + D < nslab ? sl + D : nslab - 1, rg[rd]);
+      compute(sl & 1, sl & 1);
+      if constexpr (DX == 0) issue_x(sl + 1 < nslab ? sl + 1 : nslab - 1, rx_[x1]);
+      if (sl + 1 < nslab) put(rg[r1], rx_[x1], (sl + 1) & 1);
+    };
+    int sl = 0;
+    for (; sl + kRing <= nslab; sl += kRing)
+      static_for<0, kRing>([&](auto I) __attribute__((always_inline)) { iter(sl + decltype(I)::value, I); });
+    static_for<0, kRing - 1>([&](auto I) __attribute__((always_inline)) {
+      if (sl + decltype(I)::value < nslab) iter(sl + decltype(I)::value, I);
+    });
+  }
 
   // D: lane holds rows 4 (lane / 16) + e of its 16-row tile for token lane % 16
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < NJ; ++j) {
     const int t = t0 + wtk + 16 * j + lrow;
     if (t >= m) continue;
     uint16_t* yr = y + (size_t)t * ldy;
@@ -263,18 +395,29 @@ __global__ void __launch_bounds__(kThreads, 2) wq_gemm_kernel(const uint16_t* __
   }
 }
 
+template <int BITS, int G, int R, int T, int RING, int XR, bool XM, bool DMA>
+int launch_tiles(const void* x, int m, const void* wt, const void* st, void* y, int n, int ldy, int k, hipStream_t s) {
+  const int nrt = (n + R - 1) / R, ntt = (m + T - 1) / T;
+  const long long grid = XM ? ((long long)nrt * ntt + 7) / 8 * 8 : (long long)((nrt + 7) / 8) * 8 * ntt;
+  if (grid > 0x7FFFFFFF) return AK_INVALID;
+  hipLaunchKernelGGL((wq_gemm_kernel<BITS, G, R, T, RING, XR, XM, DMA>), dim3((unsigned)grid), dim3(2 * R),
+                     DMA ? (2 * R + XR * T) * kRowBytes : kStages * (R + T) * kRowBytes, s, static_cast<const uint16_t*>(x), m,
+                     static_cast<const uint8_t*>(wt), static_cast<const uint16_t*>(st), static_cast<uint16_t*>(y), n,
+                     ldy, k, nrt, ntt);
+  return (int)hipGetLastError();
+}
+
 template <int BITS, int G>
 int launch_gemm(const void* x, int m, const void* wt, const void* st, void* y, int n, int ldy, int k, hipStream_t s) {
-  const int nrt = (n + kRows - 1) / kRows, ntt = (m + kToks - 1) / kToks;
   // 32-bit buffer offsets: the weights, scales and inputs must each stay below 2 GB
   if ((long long)kpad(k) / 1024 * n * 128 * BITS >= (1ll << 31) || (long long)m * k * 2 >= (1ll << 31))
     return AK_INVALID;
-  const long long grid = (long long)((nrt + 7) / 8) * 8 * ntt;
-  if (grid > 0x7FFFFFFF) return AK_INVALID;
-  hipLaunchKernelGGL((wq_gemm_kernel<BITS, G>), dim3((unsigned)grid), dim3(kThreads), kStages * kStage, s,
-                     static_cast<const uint16_t*>(x), m, static_cast<const uint8_t*>(wt),
-                     static_cast<const uint16_t*>(st), static_cast<uint16_t*>(y), n, ldy, k, ntt);
-  return (int)hipGetLastError();
+  // 256 x 256 tiles above 128 tokens where there are enough of them to fill the GPU (measured: from about 160 tiles
+  // on, e.g. gate_up 55296 rows from 129 tokens, the 5120-row linears from 2048), else 128 x 128 tiles at two
+  // workgroups per CU
+  const long long big_tiles = (long long)((n + 255) / 256) * ((m + 255) / 256);
+  if (m > 128 && big_tiles >= 160) return launch_tiles<BITS, G, 256, 256, 4, 2, true, true>(x, m, wt, st, y, n, ldy, k, s);
+  return launch_tiles<BITS, G, 128, 128, 4, 4, false, false>(x, m, wt, st, y, n, ldy, k, s);
 }
 
 }  // namespace

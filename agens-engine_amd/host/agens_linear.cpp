@@ -117,15 +117,16 @@ namespace {
 int g_prefill_route = -1;  // -1: by shape, 0: dequantized tiles x library GEMM, 1: the fused GEMM
 
 // The fused prefill GEMM (ak_wq_gemm_kt) against dequantized tiles x rocBLAS, measured on MI355X (us per call):
-//   gate_up W3 55296 x 5120:  m = 256: 273 vs 381, m = 512: 500 vs 475;
-//   down W2 5120 x 27648:     m = 256: 339 vs 528, m = 512: 345 vs 390;
-//   o W4 5120 x 5120:         m = 256:  71 vs  61, m = 512:  74 vs  58.
-// The fused kernel wins on long k and on wide linears up to a few hundred tokens; the library GEMM on narrow,
-// short-k linears (too few 128 x 128 tiles for the CUs) and at large m (the fused kernel expands every weight once per
-// 128 tokens).
+//   gate_up W3 55296 x 5120:   m = 512: 408 vs 532, m = 1024: 775 vs 731, m = 2048: 1339 vs 1064;
+//   LM head W4 152064 x 5120:  m = 1024: 1709 vs 1957, m = 2048: 3244 vs 2894;
+//   down W2 5120 x 27648:      m = 512: 349 vs 392, m = 1024: 479 vs 501, m = 2048: 662 vs 558;
+//   o W4 5120 x 5120:          m = 256:  72 vs  59, m = 512:  75 vs  55.
+// The fused kernel wins on long k and on wide linears up to several hundred tokens; the library GEMM on narrow,
+// short-k linears (too few tiles for the CUs) and at large m (the fused kernel expands every weight once per token
+// tile).
 bool prefill_fused(int n, int k, int m) {
   if (g_prefill_route >= 0) return g_prefill_route == 1;
-  return k >= 16384 || (n >= 16384 && m <= 384);
+  return (k >= 16384 && m <= 1024) || (n >= 16384 && m <= (n >= 100000 ? 1536 : 768));
 }
 }  // namespace
 

@@ -115,3 +115,35 @@ def test_gemm_prefill_shapes_against_library_route(bits):
         a, b = bf2f_array(y).astype(np.float64), bf2f_array(y2).astype(np.float64)
         mag = np.abs(bf2f_array(x).astype(np.float64)) @ np.abs(bf2f_array(w).astype(np.float64)).T
         assert np.all(np.abs(a - b) <= 2 * (ulp_bf16(b) + mag * k * 2.0 ** -24))
+
+
+@pytest.mark.parametrize("bits", [4, 3, 2])
+@pytest.mark.parametrize("group", [128, 64])
+@pytest.mark.parametrize("m,n,k", [(257, 20557, 640), (520, 14000, 1152)])
+def test_gemm_wide_tiles_within_bound(bits, group, m, n, k):
+    """Shapes with at least 160 tiles of 256 rows x 256 tokens take the wide tiling (tokens loaded straight into LDS,
+    the dequantization interleaved with the MFMAs, XCD-contiguous tile order): ragged rows, tokens (one token past a
+    tile; 8 tokens into a third tile) and k (not a multiple of the 1024-input KT tile); sampled rows within the bound
+    of fp64, the rows near every tile edge included."""
+    L = make(8500 + bits + group, n, k, group, bits)
+    x = gen_x(8600 + m, m * k).reshape(m, k)
+    y = gemm(L, Dev.of(x), m)
+    rows = np.unique(np.r_[0:96, 250:262, n // 2 - 40:n // 2 + 40, n - 300:n])
+    w = dequant_host(L)
+    assert within(y[:, rows], x, w[rows], k) <= 1.0
+
+
+@pytest.mark.parametrize("bits", [4, 3, 2])
+def test_gemm_wide_tiles_exact_on_small_integer_operands(bits):
+    """The wide tiling on small-integer operands and power-of-two scales: bit-exact against the fp64 product on every
+    output (pins its operand layouts, the token DMA slots and the tile order), ldy stride padding untouched."""
+    m, n, k, g = 300, 20600, 1024, 128
+    L = make(8700 + bits, n, k, g, bits, scale_pow2=True)
+    rng = np.random.default_rng(8701)
+    x = f2bf_array(rng.integers(-3, 4, (m, k)).astype(np.float32))
+    ld = n + 24
+    y = gemm(L, Dev.of(x), m, ldy=ld, fill=0x7FC1)
+    w = dequant_host(L)
+    ref = bf2f_array(x).astype(np.float64) @ bf2f_array(w).astype(np.float64).T
+    assert np.array_equal(y[:, :n], f2bf_array(ref.astype(np.float32)))
+    assert (y[:, n:] == 0x7FC1).all()
