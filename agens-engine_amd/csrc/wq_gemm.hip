@@ -29,6 +29,7 @@
 // token l % 16 (the same input-to-slot map for weights and tokens, which is all an MFMA needs).
 // The accumulation order is this kernel's own (fp32 MFMA sums over 32 inputs, slabs in order): results agree with the
 // reference's cuBLAS route and with the oracle's dequantized weights times x in fp64 within fp32-accumulation error.
+#include <algorithm>
 #include <type_traits>
 
 #include "agens_kernels.h"
@@ -36,6 +37,8 @@
 
 
 namespace agq {
+void* stream_scratch(hipStream_t s, size_t bytes);
+
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -119,12 +122,12 @@ __device__ __forceinline__ u32x4 dequant8(uint32_t w, float s) {
 // loads of the weights RING - 1 slabs ahead and of the tokens XR - 1 slabs ahead (RING a multiple of XR); XM: the
 // XCD-contiguous tile order (below); DMA: the tokens are loaded straight into XR LDS stages of their own (buffer
 // loads into LDS), not through registers
-template <int BITS, int G, int R, int T, int RING, int XR, bool XM, bool DMA>
+template <int BITS, int G, int R, int T, int RING, int XR, bool XM, bool DMA, bool SPLIT>
 __global__ void __launch_bounds__(2 * R, R == 128 ? 2 : 1) wq_gemm_kernel(const uint16_t* __restrict__ x, int m,
                                                               const uint8_t* __restrict__ wt,
                                                               const uint16_t* __restrict__ st,
                                                               uint16_t* __restrict__ y, int n, int ldy, int k,
-                                                              int nrow_tiles, int ntok_tiles) {
+                                                              int nrow_tiles, int ntok_tiles, float* __restrict__ part) {
   constexpr int kRows = R, kToks = T, kThreads = 2 * R, kRing = RING;
   // LDS: DMA: two weight stages of R rows, then XR token stages of T tokens; else two stages of R rows + T tokens
   constexpr int kStage = DMA ? R * kRowBytes : (R + T) * kRowBytes, kXBase = DMA ? 2 * kStage : R * kRowBytes;
@@ -160,7 +163,10 @@ __global__ void __launch_bounds__(2 * R, R == 128 ? 2 : 1) wq_gemm_kernel(const 
   constexpr int REC = 128 * BITS, CB = BITS == 4 ? 16 : 8;  // record bytes; bytes of a lane chunk's (low) words
   const int lr = tid >> 1, lj = tid & 1;
   const int orow = o0 + lr < n ? o0 + lr : n - 1;
-  const int nslab = k / kSlab;
+  // split-K (part != nullptr): workgroup (.., blockIdx.y) takes slabs [sb, sb + nslab) of the k range and writes its
+  // fp32 tile to part[blockIdx.y][token][row] (row stride n); a second kernel adds the splits in order
+  const int sb = SPLIT ? (int)((long long)blockIdx.y * (k / kSlab) / gridDim.y) : 0;
+  const int nslab = SPLIT ? (int)((long long)(blockIdx.y + 1) * (k / kSlab) / gridDim.y) - sb : k / kSlab;
   // buffer loads: a per-lane offset fixed for the whole loop plus a per-slab scalar offset (no address arithmetic on
   // the vector unit in the loop); every buffer is below 2 GB (checked by the launcher)
   const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(wt), (short)0, 0x7FFFFFFF,
@@ -201,7 +207,7 @@ __global__ void __launch_bounds__(2 * R, R == 128 ? 2 : 1) wq_gemm_kernel(const 
   WSlab rg[kRing];
   XSlab rx_[DMA ? 1 : XR];
   auto issue_w = [&](int sl, WSlab& d) __attribute__((always_inline)) {
-    const int t = sl >> 4, s16 = sl & 15;  // tile, slab within the tile
+    const int t = (sb + sl) >> 4, s16 = (sb + sl) & 15;  // tile, slab within the tile
     const int tb = t * n * REC;
     if constexpr (BITS == 4) {
       d.w.w = __builtin_amdgcn_raw_buffer_load_b128(rw, vw, tb + s16 * 32, 0);
@@ -216,14 +222,14 @@ __global__ void __launch_bounds__(2 * R, R == 128 ? 2 : 1) wq_gemm_kernel(const 
   auto issue_x = [&](int sl, XSlab& d) __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < XPT; ++j)
-      if constexpr (!DMA) d.xv[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, vx[j], sl * kSlab * 2, 0);
+      if constexpr (!DMA) d.xv[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, vx[j], (sb + sl) * kSlab * 2, 0);
   };
   // DMA: slab sl's tokens into token stage xs (every wave its XPT blocks)
   auto dma_x = [&](int sl, int xs) __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < XPT; ++j)
       lds_dma16(rx, lds + kXBase + xs * kXStage + (wave + (kThreads / 64) * j) * 1024,
-                vx[0] + j * (kThreads / 64) * 8 * k * 2, sl * kSlab * 2);
+                vx[0] + j * (kThreads / 64) * 8 * k * 2, (sb + sl) * kSlab * 2);
   };
   // (the zero selection of tokens past m happens here, at the write: selecting at the load would wait for the data)
   auto put = [&](const WSlab& d, const XSlab& dx, int stage) __attribute__((always_inline)) {
@@ -384,6 +390,21 @@ __global__ void __launch_bounds__(2 * R, R == 128 ? 2 : 1) wq_gemm_kernel(const 
   for (int j = 0; j < NJ; ++j) {
     const int t = t0 + wtk + 16 * j + lrow;
     if (t >= m) continue;
+    if (SPLIT) {  // the fp32 tile
+      float* pr = part + ((size_t)blockIdx.y * m + t) * n;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r0 = o0 + wr + 16 * i + 4 * lsub;
+        if ((n & 3) == 0 && r0 < n) {
+          *reinterpret_cast<f32x4*>(pr + r0) = acc[i][j];
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (r0 + e < n) pr[r0 + e] = acc[i][j][e];
+        }
+      }
+      continue;
+    }
     uint16_t* yr = y + (size_t)t * ldy;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -395,15 +416,40 @@ __global__ void __launch_bounds__(2 * R, R == 128 ? 2 : 1) wq_gemm_kernel(const 
   }
 }
 
-template <int BITS, int G, int R, int T, int RING, int XR, bool XM, bool DMA>
-int launch_tiles(const void* x, int m, const void* wt, const void* st, void* y, int n, int ldy, int k, hipStream_t s) {
+// y[t][o] = bf16(part[0][t][o] + part[1][t][o] + ... + part[S - 1][t][o]), the splits in order; 4 rows per thread
+__global__ void __launch_bounds__(256) sum_splits_kernel(const float* __restrict__ part, int nsplit, int m, int n,
+                                                         uint16_t* __restrict__ y, int ldy) {
+  const int n4 = (n + 3) >> 2;
+  const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (long long)m * n4) return;
+  const int t = (int)(i / n4), o = (int)(i - (long long)t * n4) * 4;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int sp = 0; sp < nsplit; ++sp) {
+    const float* pr = part + ((size_t)sp * m + t) * n + o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (o + e < n) acc[e] += pr[e];
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    if (o + e < n) y[(size_t)t * ldy + o + e] = __builtin_bit_cast(uint16_t, (__bf16)acc[e]);
+}
+
+template <int BITS, int G, int R, int T, int RING, int XR, bool XM, bool DMA, bool SPLIT = false>
+int launch_tiles(const void* x, int m, const void* wt, const void* st, void* y, int n, int ldy, int k, hipStream_t s,
+                 int nsplit = 1, float* part = nullptr) {
   const int nrt = (n + R - 1) / R, ntt = (m + T - 1) / T;
   const long long grid = XM ? ((long long)nrt * ntt + 7) / 8 * 8 : (long long)((nrt + 7) / 8) * 8 * ntt;
   if (grid > 0x7FFFFFFF) return AK_INVALID;
-  hipLaunchKernelGGL((wq_gemm_kernel<BITS, G, R, T, RING, XR, XM, DMA>), dim3((unsigned)grid), dim3(2 * R),
+  hipLaunchKernelGGL((wq_gemm_kernel<BITS, G, R, T, RING, XR, XM, DMA, SPLIT>), dim3((unsigned)grid, (unsigned)nsplit), dim3(2 * R),
                      DMA ? (2 * R + XR * T) * kRowBytes : kStages * (R + T) * kRowBytes, s, static_cast<const uint16_t*>(x), m,
                      static_cast<const uint8_t*>(wt), static_cast<const uint16_t*>(st), static_cast<uint16_t*>(y), n,
-                     ldy, k, nrt, ntt);
+                     ldy, k, nrt, ntt, part);
+  if (nsplit > 1) {
+    const long long items = (long long)m * ((n + 3) / 4);
+    hipLaunchKernelGGL(sum_splits_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, s, part, nsplit, m, n,
+                       static_cast<uint16_t*>(y), ldy);
+  }
   return (int)hipGetLastError();
 }
 
@@ -417,6 +463,20 @@ int launch_gemm(const void* x, int m, const void* wt, const void* st, void* y, i
   // workgroups per CU
   const long long big_tiles = (long long)((n + 255) / 256) * ((m + 255) / 256);
   if (m > 128 && big_tiles >= 160) return launch_tiles<BITS, G, 256, 256, 4, 2, true, true>(x, m, wt, st, y, n, ldy, k, s);
+  // 128 x 128 tiles; where there are fewer than 384 (measured: below that, splitting k wins over the partials'
+  // extra traffic), k is split across workgroups up to 512 of them (at least 8 slabs per split): fp32 partial tiles in
+  // the stream's scratch after its first 4 KB (the GEMV kernels' row-range counters, which stay zero between
+  // launches), summed in order by a second kernel; one pass where the scratch is not available (e.g. first use under
+  // stream capture)
+  const long long tiles = (long long)((n + 127) / 128) * ((m + 127) / 128);
+  int nsplit = 1;
+  if (tiles < 384) nsplit = (int)std::min<long long>((512 + tiles - 1) / tiles, std::min(64, k / kSlab / 8));
+  float* part = nullptr;
+  if (nsplit > 1) {
+    if (void* z = stream_scratch(s, 4096 + (size_t)nsplit * m * n * 4))
+      part = reinterpret_cast<float*>(static_cast<uint8_t*>(z) + 4096);
+  }
+  if (part) return launch_tiles<BITS, G, 128, 128, 4, 4, false, false, true>(x, m, wt, st, y, n, ldy, k, s, nsplit, part);
   return launch_tiles<BITS, G, 128, 128, 4, 4, false, false>(x, m, wt, st, y, n, ldy, k, s);
 }
 

@@ -13,8 +13,8 @@ import ctypes
 import numpy as np
 import pytest
 
-from _lib import (kernels, check, Dev, Linear, gen_container, gen_scales, gen_x, oracle, ptr, bf2f_array, f2bf_array,
-                  ulp_bf16)
+from _lib import (kernels, check, Dev, Linear, gemv, gen_container, gen_scales, gen_x, oracle, ptr, bf2f_array,
+                  f2bf_array, ulp_bf16)
 
 pytestmark = pytest.mark.gpu
 
@@ -147,3 +147,25 @@ def test_gemm_wide_tiles_exact_on_small_integer_operands(bits):
     ref = bf2f_array(x).astype(np.float64) @ bf2f_array(w).astype(np.float64).T
     assert np.array_equal(y[:, :n], f2bf_array(ref.astype(np.float32)))
     assert (y[:, n:] == 0x7FC1).all()
+
+
+def test_split_k_gemm_leaves_gemv_scratch_intact():
+    """A narrow long-k GEMM splits k across workgroups (fp32 partials in the stream's scratch); the split-K GEMV
+    launches on the same stream keep their row-range counters in the first 4 KB of that scratch, zero between
+    launches: a 4-token down-shaped GEMV (5120 x 27648, split-K route) gives the same bits before and after it."""
+    K = kernels()
+    k = 27648
+    D = make(8800, 5120, k, 128, 2)
+    xg = gen_x(8801, 4 * k, 0.5)
+    before = gemv(2, Dev.of(xg), 4, [D], k, 128)[0]
+    check(K.ak_synchronize(), "sync")
+    a = before.get(np.uint16, 4 * 5120)
+    G = make(8802, 640, k, 128, 3)
+    m = 256
+    x = gen_x(8803, m * k).reshape(m, k)
+    y = gemm(G, Dev.of(x), m)
+    rows = np.r_[0:64, 576:640]
+    assert within(y[:, rows], x, dequant_host(G)[rows], k) <= 1.0
+    after = gemv(2, Dev.of(xg), 4, [D], k, 128)[0]
+    check(K.ak_synchronize(), "sync")
+    assert np.array_equal(after.get(np.uint16, 4 * 5120), a)
