@@ -146,35 +146,40 @@ __global__ void __launch_bounds__(256) repack_kernel(const uint4* __restrict__ s
   if (BITS != 4 && my_bad) atomicOr(bad, 1);
 }
 
-// KT rows [r0, r0 + nr) -> dense bf16 w [nr][k], w = bf16_rn(q * scale) (the product is exact in fp32).
+// KT rows [r0, r0 + nr) -> dense bf16 w [nr][k], w = bf16_rn(q * scale) (the product is exact in fp32; the conversion
+// rounds to nearest even).  Thread = 8 consecutive outputs of a row (16 bytes): consecutive threads write consecutive
+// 16-byte pieces of a row and read consecutive words of its KT record (per lane chunk of 32 inputs: W4 4 words of
+// nibbles; W2 2 words of 2-bit codes; W3 those and a word of third bits, one byte per 8 inputs).
 template <int BITS, int G>
 __global__ void __launch_bounds__(256) dequant_kernel(const void* __restrict__ wt, const uint16_t* __restrict__ st,
                                                       uint16_t* __restrict__ w, int n, int k, int r0, int nr) {
   constexpr int SPT = 1024 / G, CPG = G / 32;
-  const int kc = k >> 5, tiles = kpad(k) >> 10;
-  const size_t total = (size_t)tiles * nr * 32;
+  const int kw = k >> 3;  // 16-byte pieces per output row
+  const size_t total = (size_t)nr * kw;
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
-    const int c = (int)(i & 31);
-    const size_t rl = i >> 5;
-    const int o = (int)(rl % (size_t)nr), t = (int)(rl / (size_t)nr);
-    const int cg = t * 32 + c;
-    if (cg >= kc) continue;
+    const int o = (int)(i / (size_t)kw), e = (int)(i - (size_t)o * kw);
+    const int t = e >> 7, c = (e >> 2) & 31, u = e & 3;  // 1024-input tile, lane chunk, word of the chunk
     const size_t rec = (size_t)t * n + r0 + o;
-    const uint4 q = chunk_nibbles<BITS>(wt, rec, c);
-    const float s = bf2f(st[rec * SPT + c / CPG]);
-    const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
-    uint4* out = reinterpret_cast<uint4*>(w + (size_t)o * k + (size_t)cg * 32);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      uint32_t v[4];
-#pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        const float a = (float)((int)((qw[j] >> (8 * p)) & 0xFu) - 8) * s;
-        const float b = (float)((int)((qw[j] >> (8 * p + 4)) & 0xFu) - 8) * s;
-        v[p] = (uint32_t)f2bf(a) | ((uint32_t)f2bf(b) << 16);
-      }
-      out[j] = make_uint4(v[0], v[1], v[2], v[3]);
+    const uint32_t* r = reinterpret_cast<const uint32_t*>(wt) + rec * (32 * BITS);
+    uint32_t q;  // 8 nibbles, value = nibble - 8
+    if constexpr (BITS == 4) {
+      q = r[c * 4 + u];
+    } else {
+      const uint32_t lo = spread_2to4(r[c * 2 + (u >> 1)] >> (16 * (u & 1)));
+      if constexpr (BITS == 2) q = lo + 0x66666666u;
+      else q = (lo | (spread_1to4(r[64 + c] >> (8 * u)) << 2)) + 0x44444444u;
     }
+    const float s = bf2f(st[rec * SPT + c / CPG]), m8 = -8.0f * s;
+    const uint32_t ev = q & 0x0F0F0F0Fu, od = (q >> 4) & 0x0F0F0F0Fu;  // inputs 2b, 2b + 1 in byte b
+    uint32_t v[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+      const bf16x2 p = {(__bf16)fmaf((float)((ev >> (8 * b)) & 0xFFu), s, m8),
+                        (__bf16)fmaf((float)((od >> (8 * b)) & 0xFFu), s, m8)};
+      v[b] = __builtin_bit_cast(uint32_t, p);
+    }
+    reinterpret_cast<uint4*>(w + (size_t)o * k)[e] = make_uint4(v[0], v[1], v[2], v[3]);
   }
 }
 
@@ -253,8 +258,8 @@ int ak_wq_dequant_kt_rows(int bits, const void* wt, const void* st, void* w, int
     case 2064: kern = dequant_kernel<2, 64>; break;
     default: return AK_INVALID;
   }
-  const size_t total = (size_t)(kpad(k) >> 10) * nr * 32;
-  const size_t want = (total + 255) / 256, cap = (size_t)num_cus() * 8;
+  const size_t total = (size_t)nr * (k >> 3);
+  const size_t want = (total + 255) / 256, cap = (size_t)num_cus() * 16;
   hipLaunchKernelGGL(kern, dim3((unsigned)(want < cap ? want : cap)), dim3(256), 0, static_cast<hipStream_t>(stream),
                      wt, static_cast<const uint16_t*>(st), static_cast<uint16_t*>(w), n, k, r0, nr);
   return (int)hipGetLastError();

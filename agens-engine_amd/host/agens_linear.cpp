@@ -116,18 +116,19 @@ void set_prefill_tile_bytes(size_t bytes) { g_tile_bytes = bytes; }
 namespace {
 int g_prefill_route = -1;  // -1: by shape, 0: dequantized tiles x library GEMM, 1: the fused GEMM
 
-// The fused prefill GEMM (ak_wq_gemm_kt) against dequantized tiles x rocBLAS, measured on MI355X (us per call):
-//   gate_up W3 55296 x 5120:   m = 512: 406 vs 532, m = 1024: 774 vs 731, m = 2048: 1334 vs 1064;
-//   LM head W4 152064 x 5120:  m = 1024: 1722 vs 1957, m = 2048: 3262 vs 2894;
-//   down W2 5120 x 27648:      m = 512: 227 vs 392, m = 1024: 443 vs 501, m = 2048: 676 vs 558;
-//   o W4 5120 x 5120:          m = 256:  46 vs  59, m = 512:  66 vs  55;
-//   qkv W4 7168 x 5120:        m = 256:  54 vs  85, m = 512:  78 vs  79.
+// The fused prefill GEMM (ak_wq_gemm_kt) against dequantized tiles x rocBLAS, measured on MI355X (us per call,
+// bench.py --config prefill and --config xover):
+//   gate_up W3 55296 x 5120:   m = 512: 441 vs 448, m = 2048: 1436 vs 987;
+//   LM head W4 152064 x 5120:  m = 512: 934 vs 1092, m = 2048: 3076 vs 2648;
+//   down W2 5120 x 27648:      m = 512: 239 vs 354, m = 2048: 677 vs 516;
+//   o W4 5120 x 5120:          m = 256:  46 vs  59, m = 512:  68 vs  51;
+//   qkv W4 7168 x 5120:        m = 256:  54 vs  85, m = 512:  80 vs  72.
 // The fused kernel wins on long k and on wide linears up to several hundred tokens and on every linear up to 256
 // tokens (narrow ones split k across workgroups); the library GEMM on narrow short-k linears beyond that and at large
 // m (the fused kernel expands every weight once per token tile).
 bool prefill_fused(int n, int k, int m) {
   if (g_prefill_route >= 0) return g_prefill_route == 1;
-  return m <= 256 || (k >= 16384 && m <= 1024) || (n >= 16384 && m <= (n >= 100000 ? 1536 : 768));
+  return m <= 256 || (k >= 16384 && m <= 1024) || (n >= 16384 && m <= (n >= 100000 ? 1024 : 512));
 }
 }  // namespace
 

@@ -79,7 +79,7 @@ int linear(const QuantLinear& t, const void* x, void* y, int m, int n, int k, in
 // bytes of one dequantized prefill tile (default 64 MB; the reference's tile bound, m1_model.cu:1822-1826)
 void set_prefill_tile_bytes(size_t bytes);
 // The prefill route above 128 tokens: -1 by shape (the default: the fused dequantize-in-GEMM kernel ak_wq_gemm_kt on
-// every linear up to 256 tokens, long-k linears up to 1024 and wide linears up to 768 (LM-head-wide: 1536) tokens,
+// every linear up to 256 tokens, long-k linears up to 1024 and wide linears up to 512 (LM-head-wide: 1024) tokens,
 // where it was measured faster), 0 dequantized tiles x library
 // GEMM (the reference's route), 1 the fused kernel.  Both give results within fp32-accumulation tolerance of the
 // dequantized weights times x.

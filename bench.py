@@ -12,7 +12,7 @@ reference's int4 container and repacked by ak_wq_repack_kt; inputs are resident 
 
 Effective bytes per launch = packed weights + bf16 scales + bf16 x + bf16 y (the algorithmic bytes).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--m 1] [--config sweep|0|1|2|3|i8|bi|xover] [--no-cpu] [--eager]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--m 1] [--config sweep|0|1|2|3|i8|bi|xover|prefill] [--no-cpu] [--eager]
 """
 import argparse
 import ctypes
@@ -478,6 +478,44 @@ def run_xover(args, K, B):
     return lines
 
 
+def run_prefill(args, K, B):
+    """The prefill GEMM above 128 tokens: the fused dequantize-in-GEMM kernel (ak_wq_gemm_kt) against the reference's
+    route (ak_wq_dequant_kt_rows of the whole weight, then the library GEMM ak_bf16_linear_f32reduce;
+    m1_model.cu:1876-1897) on the 32B shapes at 512 and 2048 tokens; weights rotated over >= 400 MB of copies, eager
+    calls, HIP events.  TFLOP/s = 2 m n k / time, against the 2.5 PFLOP/s bf16 dense peak."""
+    ctx = Ctx(K, B)
+    vp = ctypes.c_void_p
+    B.agb_time_xover.argtypes = [ctypes.c_int, vp, ctypes.c_int, ctypes.POINTER(vp), ctypes.POINTER(vp), ctypes.c_int,
+                                 vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                 ctypes.POINTER(ctypes.c_float)]
+    B.agb_time_xover.restype = ctypes.c_int
+    lines = []
+    for name, bits, n, k in (("gate_up_w3", 3, 55296, 5120), ("down_w2", 2, 5120, 27648), ("qkv_w4", 4, 7168, 5120),
+                             ("o_w4", 4, 5120, 5120), ("lm_head_w4", 4, 152064, 5120)):
+        lins = []
+        while sum(L.wbytes for L in lins) < 400e6:
+            lins.append(QLinear(ctx, SEED * 1000 + 900 + len(lins), n, k, bits))
+        wts = (vp * len(lins))(*[L.wt for L in lins])
+        sts = (vp * len(lins))(*[L.st for L in lins])
+        ms = (512, 2048)
+        x = ctx.alloc(max(ms) * k * 2)
+        y = ctx.alloc(max(ms) * n * 2)
+        wd = ctx.alloc(n * k * 2)
+        ctx.check(B.agb_gen_x(SEED + 43, max(ms) * k, 1.0, x, None), "gen x")
+        for m in ms:
+            row = {"config": "prefill", "linear": name, "bits": bits, "n": n, "k": k, "m": m, "copies": len(lins)}
+            for key, mode in (("fused", 2), ("dequant_gemm", 1)):
+                t = ctypes.c_float()
+                ctx.check(B.agb_time_xover(bits, x, m, wts, sts, len(lins), wd, y, n, k, mode, 2,
+                                           max(5, min(args.steps, 10)), ctypes.byref(t)), key)
+                us = t.value * 1e3
+                tf = 2.0 * m * n * k / (us * 1e-6) / 1e12
+                row[key] = {"us": round(us, 1), "TFLOPs": round(tf, 1), "frac_bf16_peak": round(tf / 2500.0, 3)}
+            lines.append(row)
+        ctx.free_all()
+    return lines
+
+
 def run_bi(args, K, B):
     """The batch-invariant bf16 GEMV (ak_bf16_gemv_bi; reference bi_gemv.cu): a 5120 x 5120 bf16 weight (weights
     rotated over >= 1 GB of copies) and a small-n projection (48 x 5120), M = 1, 16, 128."""
@@ -543,6 +581,9 @@ def main():
             print(json.dumps(line), flush=True)
     elif args.config == "xover":
         for line in run_xover(args, K, B):
+            print(json.dumps(line), flush=True)
+    elif args.config == "prefill":
+        for line in run_prefill(args, K, B):
             print(json.dumps(line), flush=True)
     elif args.config == "i8":
         for line in run_i8(args, K, B):
