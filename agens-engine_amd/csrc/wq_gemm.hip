@@ -334,13 +334,13 @@ __global__ void __launch_bounds__(2 * R, R == 128 ? 2 : 1) wq_gemm_kernel(const 
   // are needed first), compute slab sl from its stage, write slab sl + 1 (dequantized) into the other stage.
   constexpr int D = kRing - 1, DX = XR - 1;
   if constexpr (DMA) {
-    // Iteration sl: wait for this wave's token DMA of slab sl (the loads' counter is in order: at most NAFTER loads
-    // were issued after it), barrier (every wave's DMA of slab sl landed; every wave done with slab sl - 1), DMA of
-    // slab sl + DX into the token stage slab sl - 1 used, weight loads of slab sl + D, compute slab sl, write slab
-    // sl + 1's weights (dequantized) into the other weight stage.
-    constexpr int NW = BITS == 3 ? 3 : 2, NAFTER = NW + (DX - 1) * (XPT + NW);
-    static_assert(DX >= 1 && NAFTER < 64, "token DMA pipeline");
-    constexpr int kWait = (NAFTER & 15) | ((NAFTER >> 4) << 14) | (7 << 4) | (15 << 8);
+    // Iteration sl: wait for all of this wave's loads (its token DMA of slab sl among them; the weight loads still
+    // outstanding were issued a slab earlier, so this costs little, and it holds whatever order the loads were issued
+    // in), barrier (every wave's DMA of slab sl landed; every wave done with slab sl - 1), DMA of slab sl + DX into
+    // the token stage slab sl - 1 used, weight loads of slab sl + D, compute slab sl, write slab sl + 1's weights
+    // (dequantized) into the other weight stage.
+    static_assert(DX >= 1, "token DMA pipeline");
+    constexpr int kVmcnt0 = 0x0F70;  // s_waitcnt immediate: vector memory counter 0, the others unconstrained
 #pragma unroll
     for (int i = 0; i < DX; ++i) dma_x(i < nslab ? i : nslab - 1, i);
 #pragma unroll
@@ -349,7 +349,7 @@ __global__ void __launch_bounds__(2 * R, R == 128 ? 2 : 1) wq_gemm_kernel(const 
     auto iter = [&](int sl, auto S, bool last_ok) __attribute__((always_inline)) {
       constexpr int r1 = (decltype(S)::value + 1) % kRing, rd = (decltype(S)::value + D) % kRing;
       constexpr int xc = decltype(S)::value % XR, xd = (decltype(S)::value + DX) % XR;
-      __builtin_amdgcn_s_waitcnt(kWait);
+      __builtin_amdgcn_s_waitcnt(kVmcnt0);
       __syncthreads();
       dma_x(sl + DX < nslab ? sl + DX : nslab - 1, xd);
       issue_w(sl + D < nslab ? sl + D : nslab - 1, rg[rd]);
