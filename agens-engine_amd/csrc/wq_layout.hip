@@ -4,6 +4,7 @@
 // are interchangeable with the reference's; the kernels are written for wave64: one thread per 16-byte lane chunk of
 // the output, consecutive threads writing consecutive chunks of a record (fully coalesced stores), grid-stride loops.
 #include <map>
+#include <vector>
 #include <mutex>
 #include <utility>
 
@@ -24,10 +25,11 @@ int num_cus() {
 }
 
 // Library scratch per (device, stream), as the reference keeps its split-K partials and counters
-// (w4_gemv.cu:2096-2118): allocated zero-filled on first use and grown when a launch needs more, never inside a stream
-// capture (null then: the caller takes a path without scratch), held until the process ends.  Launches on one stream
-// are ordered, so they share it safely; before a buffer is replaced the stream is synchronized (earlier launches may
-// still use it).  Users keep their counters at zero between launches.
+// (w4_gemv.cu:2096-2118): allocated zero-filled on first use and grown (at least doubling) when a launch needs more,
+// never inside a stream capture (null then: the caller takes a path without scratch).  Every buffer handed out is held
+// until the process ends, the replaced ones included, so launches still in flight and graphs captured before a growth
+// keep valid memory.  Launches on one stream are ordered, so they share it safely.  Users keep their counters (the
+// first 4 KB) at zero between launches.
 //
 // A caller that must not allocate (ak_wq_gemv_kt_multi_noalloc) installs a fixed buffer for the calling thread first:
 // then this returns that buffer when it is large enough and null otherwise, and never allocates.
@@ -51,18 +53,18 @@ void* stream_scratch(hipStream_t s, size_t bytes) {
     (void)hipGetLastError();
     return nullptr;
   }
-  const size_t want = bytes > ((size_t)4 << 20) ? bytes : ((size_t)4 << 20);
-  if (b.first) {
-    (void)hipStreamSynchronize(s);
-    (void)hipFree(b.first);
-    b = {nullptr, 0};
-  }
+  // at least double: a replaced buffer is kept, not freed (a graph captured before the growth still addresses it), so
+  // the retired buffers stay below the current one in total
+  size_t want = bytes > ((size_t)4 << 20) ? bytes : ((size_t)4 << 20);
+  if (b.first && want < 2 * b.second) want = 2 * b.second;
   void* p = nullptr;
   if (hipMalloc(&p, want) != hipSuccess || hipMemset(p, 0, want) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
     if (p) (void)hipFree(p);
     (void)hipGetLastError();
     return nullptr;
   }
+  static std::vector<void*> retired;
+  if (b.first) retired.push_back(b.first);
   b = {p, want};
   return p;
 }

@@ -11,12 +11,13 @@
  *     other values are hipError_t codes;
  *   - `stream` is a hipStream_t (NULL = the default stream); launches are asynchronous and stream-ordered;
  *   - bf16 tensors are passed as void* (raw 16-bit patterns), the int4 container as int32_t words;
- *   - the caller owns every buffer it passes.  The GEMV entry points own scratch only for split-K launches (long k, or
- *     few rows per CU, at more than two tokens or long k): per (device, stream), allocated zero-filled on the first
- *     such call outside a stream capture (that call synchronizes the device once), grown when a larger launch needs
- *     it, held until the process ends -- as the reference's split-K scratch (w4_gemv.cu:2096-2118).  Inside a capture
- *     they never allocate or synchronize: without scratch they take a launch that needs none (same results), so they
- *     can be captured in a hipGraph.
+ *   - the caller owns every buffer it passes.  The GEMV entry points (and ak_wq_gemm_kt on narrow linears) own scratch
+ *     only for split-K launches (long k, or few rows per CU, at more than two tokens or long k): per (device, stream),
+ *     allocated zero-filled on the first such call outside a stream capture (that call synchronizes the device once),
+ *     grown (at least doubling) when a larger launch needs it; every buffer, a replaced one included, is held until
+ *     the process ends -- as the reference's split-K scratch (w4_gemv.cu:2096-2118) -- so graphs captured before a
+ *     growth stay valid.  Inside a capture they never allocate or synchronize: without scratch they take a launch
+ *     that needs none (the GEMV: same results; the GEMM: k not split), so they can be captured in a hipGraph.
  */
 #pragma once
 #include <stddef.h>
@@ -146,8 +147,10 @@ int ak_bf16_linear_f32reduce_ld(const void* x, const void* w, void* y, int m, in
  * the pair the model's linear() runs above 128 tokens (kernels/m1/m1_model.cu:1876-1897, w4_gemv.cu:877-895,
  * bf16_linear.cu:68-80).  y[t][o] (row stride ldy; 0: n) = bf16(sum_i x[t][i] * w[o][i]) for every token t < m and
  * row o < n of a KT linear, w[o][i] = bf16_rn(q * scale) (the dequantized values, bit for bit), fp32 accumulation in
- * this kernel's order (within fp32-accumulation error of the two-call route); no scratch, no weight copy.  group in
- * {64, 128}, k % group == 0, ldy >= n, else 1. */
+ * this kernel's order (within fp32-accumulation error of the two-call route); no weight copy.  Where the linear has
+ * few output tiles (fewer than 384 of 128 rows x 128 tokens) k is split across workgroups: fp32 partials in the
+ * stream's split-K scratch (above), added in a fixed order by a second kernel, so results are deterministic for a
+ * given shape.  group in {64, 128}, k % group == 0, ldy >= n, else 1. */
 int ak_wq_gemm_kt(int bits, const void* x, int m, const void* wt, const void* st, void* y, int n, int ldy, int k,
                   int group, void* stream);
 

@@ -169,3 +169,53 @@ def test_split_k_gemm_leaves_gemv_scratch_intact():
     after = gemv(2, Dev.of(xg), 4, [D], k, 128)[0]
     check(K.ak_synchronize(), "sync")
     assert np.array_equal(after.get(np.uint16, 4 * 5120), a)
+
+
+def test_graph_captured_before_scratch_growth_replays():
+    """A split-K GEMV captured in a hipGraph addresses its stream's scratch; a later eager split-K GEMM on the same
+    stream grows that scratch (a new buffer), and the replaced buffer stays allocated: replays after the growth, with
+    new inputs each, equal eager launches."""
+    from _lib import ptr_array, int_array
+    K = kernels()
+    hip = ctypes.CDLL("libamdhip64.so")
+    vp = ctypes.c_void_p
+    k, m = 27648, 4
+    D = make(8900, 5120, k, 128, 2)
+    X, Y = Dev(m * k * 2), Dev(m * 5120 * 2)
+    G = make(8901, 640, k, 128, 3)
+    mg = 256
+    XG, YG = Dev.of(gen_x(8902, mg * k).reshape(mg, k)), Dev(mg * 640 * 2)
+    stream, graph, exe = vp(), vp(), vp()
+    assert hip.hipStreamCreate(ctypes.byref(stream)) == 0
+
+    def gemv_on(s, y):
+        rc = K.ak_wq_gemv_kt_multi(2, X.p, m, 1, ptr_array([D.wt.p]), ptr_array([D.st.p]), ptr_array([y.p]),
+                                   int_array([5120]), None, k, 128, 0, s)
+        check(rc, "ak_wq_gemv_kt_multi")
+
+    try:
+        check(K.ak_memcpy_h2d(X.p, gen_x(8903, m * k, 0.5).ctypes.data, m * k * 2), "h2d")
+        gemv_on(stream, Y)  # first split-K call on the stream: allocates its scratch
+        assert hip.hipStreamSynchronize(stream) == 0
+        assert hip.hipStreamBeginCapture(stream, ctypes.c_int(1)) == 0
+        gemv_on(stream, Y)
+        assert hip.hipStreamEndCapture(stream, ctypes.byref(graph)) == 0
+        assert hip.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, ctypes.c_size_t(0)) == 0
+        check(K.ak_wq_gemm_kt(3, XG.p, mg, G.wt.p, G.st.p, YG.p, 640, 0, k, 128, stream), "split-K GEMM")
+        assert hip.hipStreamSynchronize(stream) == 0
+        Ye = Dev(m * 5120 * 2)
+        for rep in range(3):
+            xh = gen_x(8910 + rep, m * k, 0.5)
+            check(K.ak_memcpy_h2d(X.p, xh.ctypes.data, xh.nbytes), "h2d")
+            assert hip.hipGraphLaunch(exe, stream) == 0
+            assert hip.hipStreamSynchronize(stream) == 0
+            got = Y.get(np.uint16, m * 5120)
+            gemv_on(stream, Ye)
+            assert hip.hipStreamSynchronize(stream) == 0
+            assert np.array_equal(got, Ye.get(np.uint16, m * 5120)), f"replay {rep}"
+    finally:
+        if exe:
+            hip.hipGraphExecDestroy(exe)
+        if graph:
+            hip.hipGraphDestroy(graph)
+        hip.hipStreamDestroy(stream)
