@@ -119,6 +119,45 @@ __device__ __forceinline__ u32x4 dequant8(uint32_t w, float s) {
   return u32x4{o[0], o[1], o[2], o[3]};
 }
 
+// W2 / W3 without the nibble spread: the 2-bit codes of 16 inputs (one low word of the chunk, input i at bits 2i) as
+// four words of byte codes, word p holding inputs 4 j + p in byte j (W3: the third bit, input i at bit i of the high
+// half-word, merged at bit 2 of each byte through one 1-to-2 bit spread)
+struct HalfCodes {
+  uint32_t p0, p1, p2, p3;
+};
+template <int BITS>
+__device__ __forceinline__ HalfCodes half_codes(const ChunkRaw<BITS>& d, int h) {
+  const uint32_t L = d.w[h];
+  HalfCodes c = {L & 0x03030303u, (L >> 2) & 0x03030303u, (L >> 4) & 0x03030303u, (L >> 6) & 0x03030303u};
+  if constexpr (BITS == 3) {
+    uint32_t v = (d.w[2] >> (16 * h)) & 0xFFFFu;  // third bits of inputs 16 h .. 16 h + 15; input i -> bit 2 i:
+    v = (v | (v << 8)) & 0x00FF00FFu;
+    v = (v | (v << 4)) & 0x0F0F0F0Fu;
+    v = (v | (v << 2)) & 0x33333333u;
+    v = (v | (v << 1)) & 0x55555555u;  // input 4 j + p at bit 8 j + 2 p
+    c.p0 |= (v << 2) & 0x04040404u;
+    c.p1 |= v & 0x04040404u;
+    c.p2 |= (v >> 2) & 0x04040404u;
+    c.p3 |= (v >> 4) & 0x04040404u;
+  }
+  return c;
+}
+// inputs 8 sub .. 8 sub + 7 of the half as 4 dwords of bf16 pairs bf16_rn((n - OFF) s) (as dequant8)
+template <int OFF>
+__device__ __forceinline__ u32x4 dequant_half(const HalfCodes& c, float s, int sub) {
+  const float m = -(float)OFF * s;
+  uint32_t o[4];
+#pragma unroll
+  for (int jj = 0; jj < 2; ++jj) {
+    const int sh = 8 * (2 * sub + jj);
+    const bf16x2 ab = {(__bf16)fmaf((float)((c.p0 >> sh) & 0xFFu), s, m), (__bf16)fmaf((float)((c.p1 >> sh) & 0xFFu), s, m)};
+    const bf16x2 cd = {(__bf16)fmaf((float)((c.p2 >> sh) & 0xFFu), s, m), (__bf16)fmaf((float)((c.p3 >> sh) & 0xFFu), s, m)};
+    o[2 * jj] = __builtin_bit_cast(uint32_t, ab);
+    o[2 * jj + 1] = __builtin_bit_cast(uint32_t, cd);
+  }
+  return u32x4{o[0], o[1], o[2], o[3]};
+}
+
 // R output rows x T tokens per workgroup (2 R threads: a thread pair per row), wave tiles of 64 rows x WT tokens,
 // loads of the weights RING - 1 slabs ahead and of the tokens XR - 1 slabs ahead (RING a multiple of XR); XM: the
 // XCD-contiguous tile order (below); DMA: the tokens are loaded straight into XR LDS stages of their own (buffer
@@ -235,12 +274,20 @@ __global__ void __launch_bounds__(2 * R, R == 128 ? 2 : 1) wq_gemm_kernel(const 
   // (the zero selection of tokens past m happens here, at the write: selecting at the load would wait for the data)
   auto put = [&](const WSlab& d, const XSlab& dx, int stage) __attribute__((always_inline)) {
     uint8_t* base = lds + stage * kStage;
-    uint32_t nw[4];
-    chunk_codes<BITS>(d.w, nw);
     const float s = bf2f(d.w.s);
+    if constexpr (BITS == 4) {
+      uint32_t nw[4];
+      chunk_codes<BITS>(d.w, nw);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      *reinterpret_cast<u32x4*>(base + swz(lr, 4 * lj + u)) = dequant8<OFF>(nw[u], s);
+      for (int u = 0; u < 4; ++u) *reinterpret_cast<u32x4*>(base + swz(lr, 4 * lj + u)) = dequant8<OFF>(nw[u], s);
+    } else {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const HalfCodes hc = half_codes<BITS>(d.w, h);
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub)
+          *reinterpret_cast<u32x4*>(base + swz(lr, 4 * lj + 2 * h + sub)) = dequant_half<OFF>(hc, s, sub);
+      }
     }
     if constexpr (DMA) return;
     uint8_t* xb = lds + kXBase + stage * kXStage;
@@ -296,11 +343,13 @@ __global__ void __launch_bounds__(2 * R, R == 128 ? 2 : 1) wq_gemm_kernel(const 
     const uint8_t* B = lds + kXBase + xs * kXStage;
     uint8_t* base = lds + wstage * kStage;
     uint32_t nw[4];
-    chunk_codes<BITS>(d.w, nw);
+    if constexpr (BITS == 4) chunk_codes<BITS>(d.w, nw);
     const float sc = bf2f(d.w.s);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int q = 4 * h + lsub;
+      HalfCodes hc;
+      if constexpr (BITS != 4) hc = half_codes<BITS>(d.w, h);
       bf16x8 av[4], bv[NJ];
 #pragma unroll
       for (int i = 0; i < 4; ++i) av[i] = *reinterpret_cast<const bf16x8*>(A + swz(wr + 16 * i + lrow, q));
@@ -317,7 +366,10 @@ __global__ void __launch_bounds__(2 * R, R == 128 ? 2 : 1) wq_gemm_kernel(const 
           for (int j = 0; j < NJ; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[i], bv[j], acc[i][j], 0, 0, 0);
         const int u = 2 * h + ih;
-        *reinterpret_cast<u32x4*>(base + swz(lr, 4 * lj + u)) = dequant8<OFF>(nw[u], sc);
+        if constexpr (BITS == 4)
+          *reinterpret_cast<u32x4*>(base + swz(lr, 4 * lj + u)) = dequant8<OFF>(nw[u], sc);
+        else
+          *reinterpret_cast<u32x4*>(base + swz(lr, 4 * lj + u)) = dequant_half<OFF>(hc, sc, ih);
         static_for<0, 2 * NJ>([&](auto) __attribute__((always_inline)) {
           __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);
           __builtin_amdgcn_sched_group_barrier(0x0002, 3, 0);  // 1 MFMA, 3 VALU
