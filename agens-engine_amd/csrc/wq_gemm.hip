@@ -4,7 +4,8 @@
 // The reference's prefill route (kernels/m1/m1_model.cu:1876-1897) dequantizes a tile of output rows into a bf16
 // scratch (2 bytes per weight written, then read again) and runs a library GEMM (ak_bf16_linear_f32reduce_ld,
 // kernels/src/bf16_linear.cu:68-92).  Here the KT records are read once per token tile, expanded to bf16 in registers
-// and written to LDS, and v_mfma_f32_16x16x32_bf16 consumes them there: no scratch, no second pass over the weights.
+// and written to LDS, and v_mfma_f32_16x16x32_bf16 consumes them there: no dequantized copy, no second pass over the
+// weights (narrow linears split k across workgroups, with fp32 partials in the stream's split-K scratch).
 //
 // Two tilings, one kernel template (wq_gemm_kernel<BITS, G, R, T, RING, XR, XM, DMA>); k is walked in 64-input slabs.
 //   - 128 x 128 (R = T = 128; 256 threads, 4 waves, two workgroups per CU), where few tiles exist (narrow linears):
