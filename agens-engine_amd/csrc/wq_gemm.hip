@@ -482,6 +482,22 @@ __global__ void __launch_bounds__(256) sum_splits_kernel(const float* __restrict
   if (i >= (long long)m * n4) return;
   const int t = (int)(i / n4), o = (int)(i - (long long)t * n4) * 4;
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  if ((n & 3) == 0) {  // 16-byte partial loads, one 8-byte store
+    for (int sp = 0; sp < nsplit; ++sp) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(part + ((size_t)sp * m + t) * n + o);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[e] += v[e];
+    }
+    const bf16x2 lo = {(__bf16)acc[0], (__bf16)acc[1]}, hi = {(__bf16)acc[2], (__bf16)acc[3]};
+    uint16_t* yo = y + (size_t)t * ldy + o;
+    if ((ldy & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & 7) == 0) {  // 8-byte aligned (y may be a column offset)
+      *reinterpret_cast<uint2*>(yo) = make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) yo[e] = __builtin_bit_cast(uint16_t, (__bf16)acc[e]);
+    }
+    return;
+  }
   for (int sp = 0; sp < nsplit; ++sp) {
     const float* pr = part + ((size_t)sp * m + t) * n + o;
 #pragma unroll
