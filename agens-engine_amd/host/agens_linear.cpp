@@ -121,8 +121,8 @@ int g_prefill_route = -1;  // -1: by shape, 0: dequantized tiles x library GEMM,
 //   gate_up W3 55296 x 5120:   m = 512: 441 vs 448, m = 2048: 1436 vs 987;
 //   LM head W4 152064 x 5120:  m = 512: 934 vs 1092, m = 2048: 3076 vs 2648;
 //   down W2 5120 x 27648:      m = 512: 239 vs 354, m = 2048: 677 vs 516;
-//   o W4 5120 x 5120:          m = 256:  46 vs  59, m = 512:  68 vs  51;
-//   qkv W4 7168 x 5120:        m = 256:  54 vs  85, m = 512:  80 vs  72.
+//   o W4 5120 x 5120:          m = 256:  41 vs  59, m = 512:  58 vs  51;
+//   qkv W4 7168 x 5120:        m = 256:  49 vs  85, m = 512:  70 vs  72.
 // The fused kernel wins on long k and on wide linears up to several hundred tokens and on every linear up to 256
 // tokens (narrow ones split k across workgroups); the library GEMM on narrow short-k linears beyond that and at large
 // m (the fused kernel expands every weight once per token tile).
