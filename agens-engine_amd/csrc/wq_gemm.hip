@@ -17,9 +17,9 @@
 //   - 256 x 256 (R = T = 256; 512 threads, 8 waves, one workgroup per CU), where the tiles fill the GPU (wide linears,
 //     or from 2048 tokens): each weight is dequantized once per 256 tokens.  The tokens go straight from the buffer
 //     into LDS (buffer loads into LDS, two stages of 32 KB, one slab ahead; no registers), the weights through a
-//     register ring 3 slabs ahead into two 32 KB stages; the next slab's dequantization is interleaved with this
-//     slab's MFMAs (after each 16 MFMAs one of its four words; one MFMA, three VALU instructions alternating), since
-//     the two waves of a SIMD leave the slab's barrier together.  Grid: the tiles in token-major order cut into 8
+//     register ring (W4 / W2 3 slabs ahead, W3 1) into two 32 KB stages; the next slab's dequantization is
+//     interleaved with this slab's MFMAs (after each 16 MFMAs one of its four words; one MFMA, three VALU instructions
+//     alternating), since the two waves of a SIMD leave the slab's barrier together.  Grid: the tiles in token-major order cut into 8
 //     contiguous runs, XCD x taking run x, so that each XCD works on one or two token tiles (256 tokens x k inputs)
 //     that stay in its L2 while the weights stream.
 // Common: raw buffer loads with a per-lane offset fixed for the kernel and a scalar per-slab offset keep address
@@ -536,7 +536,10 @@ int launch_gemm(const void* x, int m, const void* wt, const void* st, void* y, i
   // on, e.g. gate_up 55296 rows from 129 tokens, the 5120-row linears from 2048), else 128 x 128 tiles at two
   // workgroups per CU
   const long long big_tiles = (long long)((n + 255) / 256) * ((m + 255) / 256);
-  if (m > 128 && big_tiles >= 160) return launch_tiles<BITS, G, 256, 256, 4, 2, true, true>(x, m, wt, st, y, n, ldy, k, s);
+  // (the weights 3 slabs ahead for W4 / W2, 1 for W3: a deeper ring spills W3's registers, measured 10 % slower; W4 /
+  // W2 are 5-11 % slower with 1)
+  if (m > 128 && big_tiles >= 160)
+    return launch_tiles<BITS, G, 256, 256, BITS == 3 ? 2 : 4, 2, true, true>(x, m, wt, st, y, n, ldy, k, s);
   // 128 x 128 tiles; where there are fewer than 384 (measured: below that, splitting k wins over the partials'
   // extra traffic), k is split across workgroups up to 512 of them (at least 8 slabs per split): fp32 partial tiles in
   // the stream's scratch after its first 4 KB (the GEMV kernels' row-range counters, which stay zero between
